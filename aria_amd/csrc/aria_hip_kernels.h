@@ -1,0 +1,88 @@
+/*
+ * aria_hip_kernels.h - internal: C-callable launchers of the gfx950 kernels.
+ *
+ * The .hip translation units own the kernels and expose one launcher each; the
+ * C host backend (aria_hip.c) validates shapes, then calls these. Every
+ * launcher takes device pointers and a HIP stream, enqueues work and returns
+ * the hipError_t of the launch (0 = success). None of them allocates.
+ */
+#ifndef ARIA_HIP_KERNELS_H
+#define ARIA_HIP_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Row normalisation with optional fused epilogue (k_rownorm.hip).
+ * norm: 0 RMSNorm y=(x*inv)*w, 1 Gemma y=(x*inv)*(1+w), 2 LayerNorm y=n*g+b.
+ * Epilogue, in this order, each optional:
+ *   scale/shift (adaLN modulate, [nbatch, dim], batch = row / rows_per_batch),
+ *   gelu (tanh GELU), resid (+ x of the same row).
+ * out_f16 != 0 stores IEEE half (RTNE) instead of float. */
+enum { ARIA_NORM_RMS = 0, ARIA_NORM_GEMMA = 1, ARIA_NORM_LAYER = 2 };
+hipError_t aria_k_rownorm(void *y, int out_f16, const float *x, const float *w, const float *b,
+                          const float *scale, const float *shift, int rows_per_batch,
+                          int gelu, int resid, int norm, int rows, int dim, float eps,
+                          hipStream_t s);
+
+/* Elementwise (k_elementwise.hip). n counts floats. */
+hipError_t aria_k_add(float *y, const float *a, const float *b, size_t n, hipStream_t s);
+hipError_t aria_k_scale(float *y, const float *x, float a, size_t n, hipStream_t s);
+hipError_t aria_k_axpy(float *y, const float *x, float a, size_t n, hipStream_t s);
+hipError_t aria_k_gelu_tanh(float *y, const float *x, size_t n, hipStream_t s);
+hipError_t aria_k_silu(float *y, const float *x, size_t n, hipStream_t s);
+hipError_t aria_k_softcap(float *y, const float *x, float cap, size_t n, hipStream_t s);
+hipError_t aria_k_silu_gate(float *out, const float *gate, const float *up, size_t n,
+                            hipStream_t s);
+hipError_t aria_k_dynamic_tanh(float *y, const float *x, float alpha, const float *w,
+                               const float *b, int rows, int dim, hipStream_t s);
+/* y = x*(1+scale[batch])+shift[batch], [rows, dim], batch = row / rows_per_batch. */
+hipError_t aria_k_modulate(float *y, const float *x, const float *scale, const float *shift,
+                           int rows, int dim, int rows_per_batch, hipStream_t s);
+/* out = res + (o [+ bias]) * sigmoid(1 - gate[batch]); gate [nbatch, dim]. */
+hipError_t aria_k_gate_residual(float *out, const float *res, const float *o,
+                                const float *gate, const float *bias, int rows, int dim,
+                                int rows_per_batch, hipStream_t s);
+/* out[r, i] = silu(proj[r, inner+i] (+b)) * (proj[r, i] (+b)); out_f16 stores half. */
+hipError_t aria_k_glu_combine(void *out, int out_f16, const float *proj, const float *bias,
+                              int rows, int inner, hipStream_t s);
+/* x = (1-tn)*(x - tc*v) + tn*noise, each op rounded on its own. */
+hipError_t aria_k_pingpong(float *x, const float *v, const float *noise, float tc, float tn,
+                           size_t n, hipStream_t s);
+/* fp32 -> fp16 (RTNE), n elements. */
+hipError_t aria_k_f32_to_f16(uint16_t *y, const float *x, size_t n, hipStream_t s);
+
+/* Row softmax in place with optional additive mask [rows, cols] (k_softmax.hip). */
+hipError_t aria_k_softmax(float *x, int rows, int cols, const float *mask, hipStream_t s);
+
+/* Rotate-half RoPE in place on x [H, N, D]; tables [N, rot/2] (k_rope.hip). */
+hipError_t aria_k_rope(float *x, const float *cos_t, const float *sin_t, int H, int N, int D,
+                       int rot_dim, hipStream_t s);
+
+/* Quantisation (k_quant.hip). Layouts are the reference's aria_quant.h ones. */
+hipError_t aria_k_q8_quant(int8_t *q, float *scale, const float *W, int N, int K, hipStream_t s);
+hipError_t aria_k_q4_quant(uint8_t *q, float *scale, const float *W, int N, int K,
+                           hipStream_t s);
+hipError_t aria_k_q8_dequant(float *W, const int8_t *q, const float *scale, int N, int K,
+                             hipStream_t s);
+hipError_t aria_k_q4_dequant(float *W, const uint8_t *q, const float *scale, int N, int K,
+                             hipStream_t s);
+
+/* fp32 SIMT GEMM (k_sgemm.hip), batched with element strides sA/sB/sC:
+ * C_b[M,N] = alpha * (A_b[M,K] op(B_b)) (+ bias[N]); op(B) = B^T for B_b [N,K]
+ * (transB = 1, Linear layout) or B for B_b [K,N] (transB = 0). */
+hipError_t aria_k_sgemm(float *C, const float *A, const float *B, const float *bias, int M, int N,
+                        int K, int transB, float alpha, int batch, long long sA, long long sB,
+                        long long sC, hipStream_t s);
+/* conv1d stride 1, zero padding (k_sgemm.hip). */
+hipError_t aria_k_conv1d(float *out, const float *in, const float *w, const float *bias, int Cin,
+                         int Cout, int K, int pad, int L, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ARIA_HIP_KERNELS_H */

@@ -1,0 +1,151 @@
+/*
+ * aria_hip.h - device-pointer, stream-ordered entry points of the MI355X backend
+ * (libaria_hip.so), beside the reference-compatible ABI in aria_gpu.h.
+ *
+ * These are the hot-path operations the reference's device DiT composes inside
+ * src/aria_cuda.cu (fused norm+modulate, gate+residual, GLU, softmax, RoPE, Q8/Q4
+ * dequant-on-use GEMM, pingpong), exposed one by one so that a caller holding
+ * device buffers can chain them on one stream with no host round trip, and the
+ * host-pointer forms of the quantizer/GEMM interfaces of src/aria_quant.h.
+ *
+ * Conventions:
+ *   - Pointers named d* or taking "device" in the comment are device memory;
+ *     all others are host memory.
+ *   - stream: a hipStream_t passed as void*; NULL means the library's own stream
+ *     (aria_hip_default_stream()). Device-pointer calls only enqueue work.
+ *   - Return value: 0 on success, a negative ARIA_HIP_E* code on a rejected
+ *     argument, or the positive hipError_t of a failed HIP call.
+ *     aria_hip_last_error() describes the last failure.
+ *   - Shapes are row-major fp32 unless stated; weights are PyTorch Linear
+ *     [N = out, K = in] (src/aria_ops.h:10).
+ *   - rows_per_batch: per-batch broadcast vectors (adaLN scale/shift/gate) are
+ *     [rows / rows_per_batch, dim]; row r uses vector r / rows_per_batch.
+ */
+#ifndef ARIA_HIP_H
+#define ARIA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ARIA_HIP_EINVAL  (-1)   /* bad shape, NULL where a buffer is required */
+#define ARIA_HIP_ENODEV  (-2)   /* no usable HIP device */
+#define ARIA_HIP_ENOMEM  (-3)   /* device allocation failed */
+
+/* ---- runtime ---- */
+/* Select device 0 and create the library stream; idempotent, thread-safe.
+ * Returns 0, or ARIA_HIP_ENODEV. Every other call initialises on demand. */
+int aria_hip_init(void);
+const char *aria_hip_last_error(void);
+void *aria_hip_default_stream(void);
+int aria_hip_stream_sync(void *stream);
+/* HIP events for stream-ordered timing (bench harness). */
+void *aria_hip_event_create(void);
+void aria_hip_event_destroy(void *ev);
+int aria_hip_event_record(void *ev, void *stream);
+/* milliseconds between two recorded events (synchronises on the second), or -1 */
+float aria_hip_event_elapsed_ms(void *ev0, void *ev1);
+int aria_hip_memcpy_h2d_async(void *ddst, const void *hsrc, size_t bytes, void *stream);
+int aria_hip_memcpy_d2h_async(void *hdst, const void *dsrc, size_t bytes, void *stream);
+int aria_hip_memcpy_d2d_async(void *ddst, const void *dsrc, size_t bytes, void *stream);
+/* device properties: number of CUs, and the gfx target name ("gfx950") */
+int aria_hip_cu_count(void);
+int aria_hip_arch(char *buf, size_t buflen);
+
+/* ---- row normalisations (device pointers) ----
+ * Replace aria_rmsnorm / aria_gemma_rmsnorm (src/aria_ops.h:91-108,
+ * src/aria_cpu.c:643-733). LayerNorm has no reference op: biased variance,
+ * y = (x - mean)/sqrt(var + eps) * gamma + beta, gamma/beta may be NULL. */
+int aria_hip_rmsnorm_dev(float *dy, const float *dx, const float *dw, int rows, int dim,
+                         float eps, void *stream);
+int aria_hip_gemma_rmsnorm_dev(float *dy, const float *dx, const float *dw, int rows, int dim,
+                               float eps, void *stream);
+int aria_hip_layernorm_dev(float *dy, const float *dx, const float *dgamma, const float *dbeta,
+                           int rows, int dim, float eps, void *stream);
+/* Fused RMSNorm(w) -> adaLN modulate, one pass: y = (x*inv*w)*(1+scale)+shift.
+ * The reference runs aria_rmsnorm then adaln_modulate (src/aria_sa3_dit.c:175-176,
+ * 255-256); its device twin is k_rmsnorm_adaln(_h) (src/aria_cuda.cu:199-249).
+ * out_f16 != 0 writes IEEE half (the GEMM operand) into dy. */
+int aria_hip_rmsnorm_adaln_dev(void *dy, int out_f16, const float *dx, const float *dw,
+                               const float *dscale, const float *dshift, int rows, int dim,
+                               int rows_per_batch, float eps, void *stream);
+/* Config 1/2 chain fused into one pass:
+ * out = gelu_tanh(LayerNorm(x)*gamma+beta)*(1+scale)+shift) + x. */
+int aria_hip_ln_mod_gelu_res_dev(float *dout, const float *dx, const float *dgamma,
+                                 const float *dbeta, const float *dscale, const float *dshift,
+                                 int rows, int dim, int rows_per_batch, float eps, void *stream);
+
+/* ---- elementwise / broadcast (device pointers; n counts floats) ----
+ * aria_add/addto/scale/axpy, aria_silu, aria_gelu_tanh, aria_silu_gate
+ * (src/aria_ops.h:111-117,166-170); y may alias x. */
+int aria_hip_add_dev(float *dy, const float *da, const float *db, size_t n, void *stream);
+int aria_hip_axpy_dev(float *dy, const float *dx, float a, size_t n, void *stream);
+int aria_hip_scale_dev(float *dy, const float *dx, float a, size_t n, void *stream);
+int aria_hip_gelu_tanh_dev(float *dy, const float *dx, size_t n, void *stream);
+int aria_hip_silu_dev(float *dy, const float *dx, size_t n, void *stream);
+int aria_hip_silu_gate_dev(float *dout, const float *dgate, const float *dup, size_t n,
+                           void *stream);
+/* adaln_modulate (src/aria_sa3_dit.c:71-82): y = x*(1+scale)+shift. */
+int aria_hip_modulate_dev(float *dy, const float *dx, const float *dscale, const float *dshift,
+                          int rows, int dim, int rows_per_batch, void *stream);
+/* gate_sigmoid + residual (src/aria_sa3_dit.c:85-97, 211-215) as one pass:
+ * out = res + (o [+ bias]) * sigmoid(1 - gate); out may alias res. */
+int aria_hip_gate_residual_dev(float *dout, const float *dres, const float *do_,
+                               const float *dgate, const float *dbias, int rows, int dim,
+                               int rows_per_batch, void *stream);
+/* GLU combine (src/aria_sa3_dit.c:108-121): proj [rows, 2*inner] = [value | gate],
+ * out[r,i] = silu(gate (+b)) * (value (+b)); out_f16 writes half. */
+int aria_hip_glu_combine_dev(void *dout, int out_f16, const float *dproj, const float *dbias,
+                             int rows, int inner, void *stream);
+/* pingpong (src/aria_sampler.c:216-220): x = (1-tn)*(x - tc*v) + tn*noise,
+ * each operation rounded on its own: bit-identical to the host loop. */
+int aria_hip_pingpong_dev(float *dx, const float *dv, const float *dnoise, float tc, float tn,
+                          size_t n, void *stream);
+
+/* ---- softmax / rotary (device pointers) ---- */
+/* aria_softmax_inplace (src/aria_ops.h:164), mask [rows, cols] or NULL. */
+int aria_hip_softmax_dev(float *dx, int rows, int cols, const float *dmask, void *stream);
+/* aria_rope_apply (src/aria_ops.h:126): x [H, N, D] in place, tables [N, rot/2]. */
+int aria_hip_rope_apply_dev(float *dx, const float *dcos, const float *dsin, int H, int N, int D,
+                            int rot_dim, void *stream);
+
+/* ---- quantisation (src/aria_quant.h layouts) ---- */
+/* Device pack: bit-exact with aria_q8_quant / aria_q4_quant (src/aria_quant.c:78, 353). */
+int aria_hip_q8_quant_dev(int8_t *dq, float *dscale, const float *dW, int N, int K, void *stream);
+int aria_hip_q4_quant_dev(uint8_t *dq, float *dscale, const float *dW, int N, int K, void *stream);
+/* Device unpack to fp32 (the per-weight value the dequant GEMM uses). */
+int aria_hip_q8_dequant_dev(float *dW, const int8_t *dq, const float *dscale, int N, int K,
+                            void *stream);
+int aria_hip_q4_dequant_dev(float *dW, const uint8_t *dq, const float *dscale, int N, int K,
+                            void *stream);
+
+/* Host-pointer forms with the reference's signatures (src/aria_quant.h:43, 64):
+ * allocate, copy in, run, copy out, free; synchronous. Return 0 or an error. */
+int aria_hip_q8_quant(int8_t *q, float *scale, const float *W, int N, int K);
+int aria_hip_q4_quant(uint8_t *q, float *scale, const float *W, int N, int K);
+int aria_hip_q8_dequant(float *W, const int8_t *q, const float *scale, int N, int K);
+int aria_hip_q4_dequant(float *W, const uint8_t *q, const float *scale, int N, int K);
+
+/* ---- host-pointer forms of the fused ops (parity entry points) ---- */
+int aria_hip_layernorm(float *y, const float *x, const float *gamma, const float *beta,
+                       int rows, int dim, float eps);
+int aria_hip_rmsnorm_adaln(float *y, const float *x, const float *w, const float *scale,
+                           const float *shift, int rows, int dim, int rows_per_batch, float eps);
+int aria_hip_ln_mod_gelu_res(float *out, const float *x, const float *gamma, const float *beta,
+                             const float *scale, const float *shift, int rows, int dim,
+                             int rows_per_batch, float eps);
+int aria_hip_modulate(float *y, const float *x, const float *scale, const float *shift,
+                      int rows, int dim, int rows_per_batch);
+int aria_hip_gate_residual(float *out, const float *res, const float *o, const float *gate,
+                           const float *bias, int rows, int dim, int rows_per_batch);
+int aria_hip_glu_combine(float *out, const float *proj, const float *bias, int rows, int inner);
+int aria_hip_add(float *y, const float *a, const float *b, size_t n);
+int aria_hip_pingpong(float *x, const float *v, const float *noise, float tc, float tn, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ARIA_HIP_H */

@@ -1,0 +1,286 @@
+"""CPU: pins the oracle (oracle/aria_oracle.c) before it is trusted as the checker.
+
+Each function is checked against (a) the reference's own known-answer tests
+(tests/test_ops.c, tests/test_quant.c), (b) the golden vectors written by the
+compiled reference (tests/golden/ref_ops.npz), (c) the compiled reference itself
+on fresh inputs when oracle/_ref is present, and (d) closed forms / invariants /
+float64 brute force chosen so that a dropped term, wrong sign, wrong index or
+transposed operand fails.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, randn, relerr_max, rng
+
+
+# ---------------------------------------------------------------- (a) reference KATs
+
+def test_kat_test_ops(port):
+    """tests/test_ops.c:53-106, tolerance 1e-4 (tests/test_ops.c:9-15)."""
+    tol = 1e-4
+    y = port.linear(np.array([[1, 2]], np.float32), np.array([[1, 0], [0, 1], [1, 1]], np.float32),
+                    np.zeros(3, np.float32))
+    assert np.allclose(y, [[1, 2, 3]], atol=tol)
+    C = port.matmul(np.array([[1, 2, 3], [4, 5, 6]], np.float32), np.ones((3, 1), np.float32))
+    assert np.allclose(C[:, 0], [6, 15], atol=tol)
+    y = port.rmsnorm(np.array([[3.0, 4.0]], np.float32), None, 0.0)
+    assert np.allclose(y, [[0.848528, 1.131371]], atol=tol)
+    assert np.allclose(port.silu(np.array([0.0, 1.0], np.float32)), [0.0, 0.731059], atol=tol)
+    assert np.allclose(port.gelu_tanh(np.array([1.0], np.float32)), [0.841192], atol=tol)
+    assert np.allclose(port.softmax(np.array([[1.0, 2.0, 3.0]], np.float32)),
+                       [[0.090031, 0.244728, 0.665241]], atol=tol)
+    assert np.allclose(port.silu_gate(np.array([1.0], np.float32), np.array([2.0], np.float32)),
+                       [0.731059 * 2.0], atol=tol)
+
+
+# ---------------------------------------------------------------- (b) golden vectors
+
+def test_golden_bitexact(port, golden):
+    g = golden
+    assert np.array_equal(port.rmsnorm(g["rms_x"], g["rms_w"], 1e-6), g["rms_y_eps1e-6"])
+    assert np.array_equal(port.rmsnorm(g["rms_x"], None, 1e-5), g["rms_y_now_eps1e-5"])
+    assert np.array_equal(port.gemma_rmsnorm(g["rms_x"], g["gemma_w"], 1e-6), g["gemma_y"])
+    assert np.array_equal(port.rmsnorm(g["qk_x"], g["qk_w"], 1e-6), g["qk_y"])
+    assert np.array_equal(port.gelu_tanh(g["act_x"]), g["gelu_y"])
+    assert np.array_equal(port.silu(g["act_x"]), g["silu_y"])
+    assert np.array_equal(port.silu_gate(g["act_x"], g["silu_gate_up"]), g["silu_gate_y"])
+    assert np.array_equal(port.add(g["act_x"], g["add_b"]), g["add_y"])
+    for k in ("sm1", "sm2", "sm4"):
+        assert np.array_equal(port.softmax(g[k + "_x"]), g[k + "_y"]), k
+    assert np.array_equal(port.softmax(g["sm3_x"], g["sm3_m"]), g["sm3_y"])
+    for rot in (32, 64):
+        c, s = port.rope_freqs(80, rot, 10000.0)
+        assert np.array_equal(c, g[f"rope{rot}_cos"]) and np.array_equal(s, g[f"rope{rot}_sin"])
+        assert np.array_equal(port.rope_apply(g[f"rope{rot}_x"], c, s, rot), g[f"rope{rot}_y"])
+
+
+@pytest.mark.parametrize("name", ["a", "b", "c", "d"])
+def test_golden_quant(port, golden, name):
+    g = golden
+    W = g[f"qw{name}_W"]
+    q8, s8 = port.q8_quant(W)
+    assert np.array_equal(q8, g[f"qw{name}_q8"]) and np.array_equal(s8, g[f"qw{name}_s8"])
+    q4, s4 = port.q4_quant(W)
+    assert np.array_equal(q4, g[f"qw{name}_q4"]) and np.array_equal(s4, g[f"qw{name}_s4"])
+    x, b = g[f"qw{name}_x"], g[f"qw{name}_b"]
+    # the reference's x86 q4 GEMM is scalar: the restatement matches it bit for bit
+    assert np.array_equal(port.linear_q4(x, q4, s4, b), g[f"qw{name}_y4"])
+    # the reference's q8 GEMM sums in 16 AVX2 lanes: summation order only
+    assert relerr_max(port.linear_q8(x, q8, s8, b), g[f"qw{name}_y8"]) < 1e-5
+
+
+def test_golden_attention(port, golden):
+    g = golden
+    assert_close(port.attention(g["att_q"], g["att_k"], g["att_v"]), g["att_y"], 1e-5, 1e-5, "self")
+    assert_close(port.attention(g["attx_q"], g["attx_k"], g["attx_v"]), g["attx_y"], 1e-5, 1e-5, "cross")
+
+
+# ---------------------------------------------------------------- (c) compiled reference
+
+@pytest.fixture
+def R(ref):
+    if ref is None:
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    return ref
+
+
+def test_ref_fresh_inputs(port, R):
+    r = rng(7)
+    x = randn(r, (129, 768)); w = randn(r, 768, 0.5)
+    assert np.array_equal(port.rmsnorm(x, w, 1e-5), R.rmsnorm(x, w, 1e-5))
+    a = randn(r, 10007, 3.0)
+    assert np.array_equal(port.gelu_tanh(a), R.gelu_tanh(a))
+    s = randn(r, (33, 1296), 2.0)
+    assert np.array_equal(port.softmax(s), R.softmax(s))
+    W = randn(r, (50, 1000), 0.02)
+    assert all(np.array_equal(u, v) for u, v in zip(port.q8_quant(W), R.q8_quant(W)))
+    assert all(np.array_equal(u, v) for u, v in zip(port.q4_quant(W), R.q4_quant(W)))
+
+
+# ---------------------------------------------------------------- (d) closed forms
+
+def test_layernorm_closed_forms(port):
+    eps = 1e-6
+    D = 1024
+    # constant row -> (x - mu) = 0 -> beta exactly
+    g = np.full(D, 3.0, np.float32); b = np.linspace(-1, 1, D).astype(np.float32)
+    y = port.layernorm(np.full((2, D), 7.25, np.float32), g, b, eps)
+    assert np.array_equal(y, np.broadcast_to(b, (2, D)))
+    # [a, -a] pairs: mean 0, var a^2 -> +-a/sqrt(a^2+eps)
+    a = 0.75
+    x = np.tile(np.array([a, -a], np.float32), D // 2)[None, :]
+    y = port.layernorm(x, None, None, eps)
+    want = a / np.sqrt(a * a + eps)
+    assert np.allclose(y[0, 0::2], want, rtol=1e-7) and np.allclose(y[0, 1::2], -want, rtol=1e-7)
+    # gamma/beta bind after normalisation: scale and shift of the unit output
+    r = rng(3)
+    x = randn(r, (16, D), 2.0) + 5.0
+    y0 = port.layernorm(x, None, None, eps).astype(np.float64)
+    assert np.allclose(y0.mean(1), 0, atol=1e-6) and np.allclose(y0.var(1), 1, atol=1e-5)
+    gam = randn(r, D, 0.5); bet = randn(r, D, 0.5)
+    y1 = port.layernorm(x, gam, bet, eps)
+    assert np.array_equal(y1, (y0.astype(np.float32) * gam + bet).astype(np.float32))
+    # extended-precision brute force
+    xl = x.astype(np.longdouble)
+    mu = xl.mean(1, keepdims=True)
+    ref = (xl - mu) / np.sqrt(((xl - mu) ** 2).mean(1, keepdims=True) + np.longdouble(eps))
+    assert np.max(np.abs(y0 - ref.astype(np.float64))) < 1e-6
+
+
+def test_rmsnorm_invariants(port):
+    r = rng(4)
+    x = randn(r, (8, 512))
+    assert np.allclose(port.rmsnorm(8 * x, None, 0.0), port.rmsnorm(x, None, 0.0), rtol=1e-6)
+    w = randn(r, 512)
+    # gemma with w - 1 gains == rmsnorm with w, up to the rounding of (1 + (w-1))
+    assert np.allclose(port.gemma_rmsnorm(x, (w - 1).astype(np.float32), 1e-6),
+                       port.rmsnorm(x, w, 1e-6), rtol=1e-6, atol=1e-6)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-6)
+    assert np.max(np.abs(port.rmsnorm(x, None, 1e-6) - want)) < 1e-6
+
+
+def test_modulate_gate_pingpong_rounding(port):
+    r = rng(5)
+    y = randn(r, (6, 256)); sc = randn(r, 256, 0.1); sh = randn(r, 256, 0.1)
+    want = ((y * (np.float32(1) + sc)).astype(np.float32) + sh).astype(np.float32)
+    assert np.array_equal(port.adaln_modulate(y, sc, sh), want)
+    assert np.array_equal(port.adaln_modulate(y, np.zeros(256, np.float32), np.zeros(256, np.float32)), y)
+    o = randn(r, (6, 256)); res = randn(r, (6, 256))
+    # gate = 1 -> sigmoid(0) = 0.5 exactly
+    out = port.gate_residual(res, o, np.ones(256, np.float32))
+    assert np.array_equal(out, (res + o * np.float32(0.5)).astype(np.float32))
+    gate = randn(r, 256)
+    sg = (1.0 / (1.0 + np.exp(-(1.0 - gate.astype(np.float64)))))
+    assert np.allclose(port.gate_residual(res, o, gate), res + o * sg, rtol=1e-6, atol=1e-6)
+    # the fused pass equals the reference's two passes (gate_sigmoid then x += o)
+    assert np.array_equal(port.gate_residual(res, o, gate), port.add(res, port.gate_sigmoid(o, gate)))
+    # bias binds to o first; a NULL bias keeps -0.0
+    z = np.full((1, 4), -0.0, np.float32)
+    out = port.gate_residual(z, z, np.ones(4, np.float32))
+    assert np.all(np.signbit(out))
+    x = randn(r, 1000); v = randn(r, 1000); n = randn(r, 1000)
+    assert np.array_equal(port.pingpong(x, v, n, 0.0, 0.0), x)
+    tc, tn = np.float32(0.8), np.float32(0.6)
+    d = (x - (tc * v).astype(np.float32)).astype(np.float32)
+    want = ((np.float32(1) - tn) * d).astype(np.float32) + (tn * n).astype(np.float32)
+    assert np.array_equal(port.pingpong(x, v, n, float(tc), float(tn)), want.astype(np.float32))
+
+
+def test_softmax_invariants(port):
+    r = rng(6)
+    s = randn(r, (16, 300), 2.0)
+    p = port.softmax(s)
+    assert np.allclose(p.sum(1), 1.0, atol=1e-6)
+    assert np.allclose(port.softmax(s + 3.0), p, atol=1e-6)       # shift invariance
+    m = np.zeros_like(s); m[:, 290:] = -3.4e38
+    pm = port.softmax(s, m)
+    assert np.all(pm[:, 290:] == 0) and np.allclose(pm.sum(1), 1.0, atol=1e-6)
+
+
+def test_rope_invariants(port):
+    rot, D, N = 32, 64, 40
+    c, s = port.rope_freqs(N, rot, 10000.0)
+    assert np.all(c[0] == 1) and np.all(s[0] == 0)                    # position 0: identity
+    r = rng(8)
+    x = randn(r, (3, N, D))
+    y = port.rope_apply(x, c, s, rot)
+    assert np.array_equal(y[:, 0], x[:, 0])
+    assert np.array_equal(y[..., rot:], x[..., rot:])                 # dims >= rot untouched
+    rh = rot // 2
+    nx = x[..., :rh] ** 2 + x[..., rh:rot] ** 2
+    ny = y[..., :rh] ** 2 + y[..., rh:rot] ** 2
+    assert np.allclose(nx, ny, rtol=1e-5, atol=1e-6)                  # pair norm preserved
+    # R(p) applied to position-0 content rotates by angle p*inv_i: compare with float64
+    inv = 1.0 / (10000.0 ** (np.arange(rh) * 2.0 / rot))
+    ang = np.arange(N)[:, None] * inv[None, :]
+    a, b = x[..., :rh].astype(np.float64), x[..., rh:rot].astype(np.float64)
+    want_a = a * np.cos(ang) - b * np.sin(ang)
+    want_b = b * np.cos(ang) + a * np.sin(ang)
+    assert np.max(np.abs(y[..., :rh] - want_a)) < 1e-5 and np.max(np.abs(y[..., rh:rot] - want_b)) < 1e-5
+
+
+def test_quant_closed_forms(port):
+    K = 71
+    W = np.zeros((4, K), np.float32)
+    W[1] = np.linspace(-0.3, 0.5, K)             # +-amax row
+    W[2, :] = 0.125                              # constant row (every block step 0)
+    W[3] = np.linspace(0, 1, K) ** 3
+    q8, s8 = port.q8_quant(W)
+    assert s8[0] == 0 and np.all(q8[0] == 0)
+    assert q8[1].max() == 127 and q8[1, -1] == 127 and s8[1] == np.float32(0.5) / np.float32(127)
+    q4, s4 = port.q4_quant(W)
+    assert q4.shape == (4, (K + 1) // 2) and s4.shape == (4, 2 * 3)
+    assert np.all(q4[2] == 0) and np.all(s4[2, 0::2] == np.float32(0.125)) and np.all(s4[2, 1::2] == 0)
+    assert (q4[:, -1] >> 4).max() == 0           # odd K: the last high nibble is padding
+    # round trip |dequant - W| <= step/2 (tests/test_quant.c:72-82) pins nibble order and
+    # the [min, step] pair index; a swapped nibble or pair breaks it at once
+    r = rng(9)
+    W = randn(r, (24, 1031), 0.02)
+    q8, s8 = port.q8_quant(W)
+    e8 = np.abs(port.q8_dequant(q8, s8) - W) / (s8[:, None] * 0.5 + 1e-12)
+    assert e8.max() <= 1.001
+    q4, s4 = port.q4_quant(W)
+    Wd = port.q4_dequant(q4, s4, 1031)
+    step = np.repeat(s4[:, 1::2], 32, axis=1)[:, :1031]
+    assert np.all(np.abs(Wd - W) <= step * 0.5 * 1.001 + 1e-9)
+    # half-way ties round to even (lrintf): q = w/s with w = 2.5 s and 3.5 s
+    Wt = np.zeros((1, 8), np.float32)
+    Wt[0, :4] = [127.0, 2.5, 3.5, -2.5]
+    q8, s8 = port.q8_quant(Wt)
+    assert s8[0] == 1.0 and list(q8[0, :4]) == [127, 2, 4, -2]
+
+
+def test_quant_gemm_brute_force(port):
+    """Dequant-on-use GEMMs vs float64 x @ dequant(W)^T: pins operand order and scale use."""
+    r = rng(10)
+    M, K, N = 9, 200, 17
+    x = randn(r, (M, K)); W = randn(r, (N, K), 0.02); b = randn(r, N, 0.02)
+    q8, s8 = port.q8_quant(W)
+    want = x.astype(np.float64) @ port.q8_dequant(q8, s8).astype(np.float64).T + b
+    assert relerr_max(port.linear_q8(x, q8, s8, b), want) < 1e-5
+    q4, s4 = port.q4_quant(W)
+    want = x.astype(np.float64) @ port.q4_dequant(q4, s4, K).astype(np.float64).T + b
+    assert relerr_max(port.linear_q4(x, q4, s4, b), want) < 1e-5
+    # identity weights: y = x * (127 * scale) exactly per column
+    I = np.eye(K, dtype=np.float32) * 0.5
+    q8, s8 = port.q8_quant(I)
+    y = port.linear_q8(x, q8, s8)
+    assert np.allclose(y, x * np.float32(127 * s8[0]), rtol=1e-6)
+
+
+def test_linear_attention_brute_force(port):
+    r = rng(11)
+    x = randn(r, (13, 70)); W = randn(r, (21, 70)); b = randn(r, 21)
+    want = x.astype(np.float64) @ W.astype(np.float64).T + b
+    assert relerr_max(port.linear(x, W, b), want) < 1e-6
+    q = randn(r, (2, 11, 16)); k = randn(r, (2, 7, 16)); v = randn(r, (2, 7, 16))
+    s = np.einsum("hqd,hkd->hqk", q.astype(np.float64), k.astype(np.float64)) / 4.0
+    p = np.exp(s - s.max(-1, keepdims=True)); p /= p.sum(-1, keepdims=True)
+    want = np.einsum("hqk,hkd->hqd", p, v.astype(np.float64))
+    assert np.max(np.abs(port.attention(q, k, v) - want)) < 1e-5
+    # uniform scores (k = 0) -> every query gets the mean of v
+    out = port.attention(q, np.zeros_like(k), v)
+    assert np.allclose(out, np.broadcast_to(v.mean(1, keepdims=True), out.shape), atol=1e-6)
+
+
+def test_fused_chain_is_composition(port):
+    r = rng(12)
+    B, S, D = 2, 24, 256
+    x = randn(r, (B, S, D)); sc = randn(r, (B, D), 0.1); sh = randn(r, (B, D), 0.1)
+    g = (1 + randn(r, D, 0.1)).astype(np.float32); be = randn(r, D, 0.1)
+    out = port.fused_chain(x, g, be, sc, sh, 1e-6)
+    for bi in range(B):
+        h = port.layernorm(x[bi], g, be, 1e-6)
+        h = port.adaln_modulate(h, sc[bi], sh[bi])
+        h = port.gelu_tanh(h)
+        assert np.array_equal(out[bi], port.add(h, x[bi]))
+    # and against float64 textbook math
+    x64 = x.astype(np.float64)
+    mu = x64.mean(-1, keepdims=True)
+    n = (x64 - mu) / np.sqrt(x64.var(-1, keepdims=True) + 1e-6) * g + be
+    m = n * (1 + sc[:, None, :]) + sh[:, None, :]
+    gl = 0.5 * m * (1 + np.tanh(0.7978845608028654 * (m + 0.044715 * m ** 3)))
+    assert np.max(np.abs(out - (gl + x64))) < 2e-5
