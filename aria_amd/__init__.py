@@ -85,6 +85,7 @@ SIGNATURES = {
     "aria_hip_pingpong_dev": (_i, [_P, _P, _P, _f, _f, _sz, _P]),
     "aria_hip_softmax_dev": (_i, [_P, _i, _i, _P, _P]),
     "aria_hip_rope_apply_dev": (_i, [_P, _P, _P, _i, _i, _i, _i, _P]),
+    "aria_hip_rope_apply2_dev": (_i, [_P, _P, _P, _P, _i, _i, _i, _i, _P]),
     "aria_hip_q8_quant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
     "aria_hip_q4_quant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
     "aria_hip_q8_dequant_dev": (_i, [_P, _P, _P, _i, _i, _P]),

@@ -15,36 +15,91 @@
 
 #define ARIA_WAVE 64
 
-/* ---- wave64 butterfly reductions over groups of G lanes (G a power of two) ---- */
-template <int G>
-__device__ __forceinline__ float grp_sum(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, ARIA_WAVE);
+/* ---- wave64 reductions over groups of G lanes (G = 4, 8, 16, 32 or 64) ----
+ * Within a 16-lane DPP row the butterfly runs on DPP lane swizzles (quad xor 1,
+ * quad xor 2, half-row mirror, row mirror), which read the neighbour's VGPR in the
+ * same instruction with no LDS round trip. Across rows: one xor-16 shuffle for
+ * G = 32, and four readlanes of the row results for G = 64. Every lane of a
+ * group ends with the same value (each step combines a symmetric pair with a
+ * commutative operation). */
+enum { DPP_QUAD_XOR1 = 0xB1, DPP_QUAD_XOR2 = 0x4E, DPP_ROW_HALF_MIRROR = 0x141, DPP_ROW_MIRROR = 0x140 };
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), l);
+    return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+struct OpSum {
+    template <typename T> __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMax {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct OpMin {
+    __device__ __forceinline__ float operator()(float a, float b) const { return fminf(a, b); }
+};
+
+template <int G, typename Op>
+__device__ __forceinline__ float grp_reduce(float v, Op op) {
+    static_assert(G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group size");
+    v = op(v, dpp_f32<DPP_QUAD_XOR1>(v));
+    v = op(v, dpp_f32<DPP_QUAD_XOR2>(v));
+    if (G >= 8) v = op(v, dpp_f32<DPP_ROW_HALF_MIRROR>(v));
+    if (G >= 16) v = op(v, dpp_f32<DPP_ROW_MIRROR>(v));
+    if (G == 32) v = op(v, __shfl_xor(v, 16, ARIA_WAVE));
+    if (G == 64) v = op(op(readlane_f32(v, 0), readlane_f32(v, 16)), op(readlane_f32(v, 32), readlane_f32(v, 48)));
     return v;
 }
 template <int G>
-__device__ __forceinline__ double grp_sum(double v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, ARIA_WAVE);
+__device__ __forceinline__ double grp_reduce_sum_f64(double v) {
+    static_assert(G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group size");
+    v += dpp_f64<DPP_QUAD_XOR1>(v);
+    v += dpp_f64<DPP_QUAD_XOR2>(v);
+    if (G >= 8) v += dpp_f64<DPP_ROW_HALF_MIRROR>(v);
+    if (G >= 16) v += dpp_f64<DPP_ROW_MIRROR>(v);
+    if (G == 32) v += __shfl_xor(v, 16, ARIA_WAVE);
+    if (G == 64) v = (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
     return v;
 }
-template <int G>
-__device__ __forceinline__ float grp_max(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, ARIA_WAVE));
-    return v;
-}
-template <int G>
-__device__ __forceinline__ float grp_min(float v) {
-#pragma unroll
-    for (int o = G / 2; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, ARIA_WAVE));
-    return v;
+
+template <int G> __device__ __forceinline__ float grp_sum(float v) { return grp_reduce<G>(v, OpSum()); }
+template <int G> __device__ __forceinline__ double grp_sum(double v) { return grp_reduce_sum_f64<G>(v); }
+template <int G> __device__ __forceinline__ float grp_max(float v) { return grp_reduce<G>(v, OpMax()); }
+template <int G> __device__ __forceinline__ float grp_min(float v) { return grp_reduce<G>(v, OpMin()); }
+
+/* ---- exp2-based transcendentals (v_exp_f32 / v_rcp_f32, ~1 ulp each) ----
+ * exp(x) = 2^(x*log2 e); the rounding of x*log2 e gives a relative error of about
+ * |x| * 4e-8, far inside the 1e-5 gates for the ranges these ops see. */
+#define ARIA_LOG2E 1.44269504088896341f
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * ARIA_LOG2E); }
+__device__ __forceinline__ float rcp_fast(float x) { return __builtin_amdgcn_rcpf(x); }
+/* tanh(u) = 1 - 2/(1 + e^{2u}); saturates to +-1 (e^{2u} -> inf or 0), absolute
+ * error ~1e-7 near 0, which GELU consumes as (1 + tanh). */
+__device__ __forceinline__ float tanh_fast(float u) {
+    const float e = __builtin_amdgcn_exp2f(u * (2.0f * ARIA_LOG2E));
+    return 1.0f - 2.0f * rcp_fast(1.0f + e);
 }
 
 /* ---- reference formulas, evaluation order as written in the reference C ---- */
 
 /* tanh GELU, src/aria_cpu.c:742-749: inner = c*(v + ((0.044715*v)*v)*v);
- * out = (0.5*v)*(1 + tanh(inner)). */
+ * out = (0.5*v)*(1 + tanh(inner)); tanh via tanh_fast. */
 __device__ __forceinline__ float gelu_tanh_f(float v) {
     const float c = 0.7978845608028654f;
     float cube = 0.044715f * v;
@@ -52,19 +107,30 @@ __device__ __forceinline__ float gelu_tanh_f(float v) {
     cube = cube * v;
     float inner = c * (v + cube);
     float h = 0.5f * v;
-    return h * (1.0f + tanhf(inner));
+    return h * (1.0f + tanh_fast(inner));
 }
 
-/* silu, src/aria_cpu.c:735-740: v / (1 + exp(-v)). */
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+/* silu, src/aria_cpu.c:735-740: v / (1 + exp(-v)), as v * rcp(1 + exp(-v)). */
+__device__ __forceinline__ float silu_f(float v) { return v * rcp_fast(1.0f + exp_fast(-v)); }
 
 /* sigmoid(1 - g) as the DiT gate uses it (src/aria_sa3_dit.c:85-90). */
-__device__ __forceinline__ float gate_sig_f(float g) { return 1.0f / (1.0f + expf(-(1.0f - g))); }
+__device__ __forceinline__ float gate_sig_f(float g) { return rcp_fast(1.0f + exp_fast(-(1.0f - g))); }
 
 /* IEEE half, round to nearest even (== aria_float_to_half for finite values). */
 __device__ __forceinline__ uint16_t f2h_bits(float v) {
     _Float16 h = (_Float16)v;
     return __builtin_bit_cast(uint16_t, h);
+}
+
+/* non-temporal 128-bit load/store of a float4 (streamed-once data) */
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_nt(const float4 *p) {
+    f32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_nt(float4 *p, float4 o) {
+    f32x4_t v = {o.x, o.y, o.z, o.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t *>(p));
 }
 
 /* float4 element access by compile-time or run-time index */

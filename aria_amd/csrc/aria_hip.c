@@ -398,6 +398,14 @@ int aria_hip_rope_apply_dev(float *dx, const float *dc, const float *ds, int H, 
     KCK(aria_k_rope(dx, dc, ds, H, N, D, rot, pick(stream)), "k_rope");
     return 0;
 }
+int aria_hip_rope_apply2_dev(float *dq, float *dk, const float *dc, const float *ds, int H, int N, int D,
+                             int rot, void *stream) {
+    ENSURE();
+    REQ(H >= 0 && N >= 0 && D > 0 && rot >= 0 && rot <= D && rot % 2 == 0);
+    REQ(H == 0 || N == 0 || rot == 0 || (dq && dk && dc && ds && dq != dk));
+    KCK(aria_k_rope2(dq, dk, dc, ds, H, N, D, rot, pick(stream)), "k_rope2");
+    return 0;
+}
 int aria_hip_q8_quant_dev(int8_t *dq, float *dscale, const float *dW, int N, int K, void *stream) {
     ENSURE();
     REQ(N >= 0 && K > 0 && (N == 0 || (dq && dscale && dW)));

@@ -62,6 +62,9 @@ hipError_t aria_k_softmax(float *x, int rows, int cols, const float *mask, hipSt
 /* Rotate-half RoPE in place on x [H, N, D]; tables [N, rot/2] (k_rope.hip). */
 hipError_t aria_k_rope(float *x, const float *cos_t, const float *sin_t, int H, int N, int D,
                        int rot_dim, hipStream_t s);
+/* the same rotation on two tensors of one shape (q and k) in one launch; x1 may be NULL */
+hipError_t aria_k_rope2(float *x0, float *x1, const float *cos_t, const float *sin_t, int H, int N,
+                        int D, int rot_dim, hipStream_t s);
 
 /* Quantisation (k_quant.hip). Layouts are the reference's aria_quant.h ones. */
 hipError_t aria_k_q8_quant(int8_t *q, float *scale, const float *W, int N, int K, hipStream_t s);

@@ -20,10 +20,15 @@ __device__ __forceinline__ void rot1(float &a, float &b, float c, float s) {
     b = bc + as;
 }
 
-__global__ __launch_bounds__(256) void k_rope4(float *x, const float *cos_t, const float *sin_t, int N,
-                                               int D, int rh, size_t nthreads) {
+/* x0 and (when non-NULL) x1 are rotated in one launch: threads [0, nt1) take x0,
+ * [nt1, 2*nt1) take x1 (q and k share the tables and the shape). */
+__global__ __launch_bounds__(256) void k_rope4(float *x0, float *x1, const float *cos_t, const float *sin_t,
+                                               int N, int D, int rh, size_t nt1, size_t nthreads) {
     const int tpr = rh >> 2;
-    for (size_t t = (size_t)blockIdx.x * 256 + threadIdx.x; t < nthreads; t += (size_t)gridDim.x * 256) {
+    for (size_t tt = (size_t)blockIdx.x * 256 + threadIdx.x; tt < nthreads; tt += (size_t)gridDim.x * 256) {
+        const bool second = tt >= nt1;
+        const size_t t = second ? tt - nt1 : tt;
+        float *x = second ? x1 : x0;
         size_t row = t / tpr;
         int j = (int)(t % tpr) * 4;
         int p = (int)(row % (size_t)N);
@@ -39,9 +44,12 @@ __global__ __launch_bounds__(256) void k_rope4(float *x, const float *cos_t, con
     }
 }
 
-__global__ __launch_bounds__(256) void k_rope1(float *x, const float *cos_t, const float *sin_t, int N,
-                                               int D, int rh, size_t nthreads) {
-    for (size_t t = (size_t)blockIdx.x * 256 + threadIdx.x; t < nthreads; t += (size_t)gridDim.x * 256) {
+__global__ __launch_bounds__(256) void k_rope1(float *x0, float *x1, const float *cos_t, const float *sin_t,
+                                               int N, int D, int rh, size_t nt1, size_t nthreads) {
+    for (size_t tt = (size_t)blockIdx.x * 256 + threadIdx.x; tt < nthreads; tt += (size_t)gridDim.x * 256) {
+        const bool second = tt >= nt1;
+        const size_t t = second ? tt - nt1 : tt;
+        float *x = second ? x1 : x0;
         size_t row = t / rh;
         int i = (int)(t % rh);
         int p = (int)(row % (size_t)N);
@@ -53,19 +61,25 @@ __global__ __launch_bounds__(256) void k_rope1(float *x, const float *cos_t, con
     }
 }
 
-extern "C" hipError_t aria_k_rope(float *x, const float *cos_t, const float *sin_t, int H, int N, int D,
-                                  int rot_dim, hipStream_t s) {
+extern "C" hipError_t aria_k_rope2(float *x0, float *x1, const float *cos_t, const float *sin_t, int H, int N,
+                                   int D, int rot_dim, hipStream_t s) {
     const int rh = rot_dim / 2;
     if (H <= 0 || N <= 0 || rh <= 0) return hipSuccess;
     const size_t rows = (size_t)H * N;
-    const bool vec = rh % 4 == 0 && D % 4 == 0 && ((uintptr_t)x & 15u) == 0 &&
+    const bool vec = rh % 4 == 0 && D % 4 == 0 && ((uintptr_t)x0 & 15u) == 0 && ((uintptr_t)x1 & 15u) == 0 &&
                      ((uintptr_t)cos_t & 15u) == 0 && ((uintptr_t)sin_t & 15u) == 0;
-    const size_t nt = vec ? rows * (rh / 4) : rows * rh;
+    const size_t nt1 = vec ? rows * (rh / 4) : rows * rh;
+    const size_t nt = x1 ? 2 * nt1 : nt1;
     size_t blocks = (nt + 255) / 256;
     if (blocks > 256 * 64) blocks = 256 * 64;
     if (vec)
-        hipLaunchKernelGGL(k_rope4, dim3((unsigned)blocks), dim3(256), 0, s, x, cos_t, sin_t, N, D, rh, nt);
+        hipLaunchKernelGGL(k_rope4, dim3((unsigned)blocks), dim3(256), 0, s, x0, x1, cos_t, sin_t, N, D, rh, nt1, nt);
     else
-        hipLaunchKernelGGL(k_rope1, dim3((unsigned)blocks), dim3(256), 0, s, x, cos_t, sin_t, N, D, rh, nt);
+        hipLaunchKernelGGL(k_rope1, dim3((unsigned)blocks), dim3(256), 0, s, x0, x1, cos_t, sin_t, N, D, rh, nt1, nt);
     return hipGetLastError();
+}
+
+extern "C" hipError_t aria_k_rope(float *x, const float *cos_t, const float *sin_t, int H, int N, int D,
+                                  int rot_dim, hipStream_t s) {
+    return aria_k_rope2(x, nullptr, cos_t, sin_t, H, N, D, rot_dim, s);
 }

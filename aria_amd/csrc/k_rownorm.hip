@@ -6,19 +6,23 @@
  * 255-256) and the config chain LayerNorm -> modulate -> tanh-GELU -> + x.
  *
  * Mapping: a row is owned by LPR lanes of one wave64 (LPR = 64 for dim >= 256,
- * 16 for the 64-wide q/k-norm rows). Each lane loads VPL float4 (128-bit,
+ * 16/32 for the 64/128-wide q/k-norm rows). Each lane loads VPL float4 (128-bit,
  * coalesced: lane l reads vectors l, l+LPR, ...), keeps them in registers,
- * reduces the statistic in double across its LPR lanes with xor shuffles, and
- * writes the transformed row once: HBM traffic = read x + write y. No LDS, no
- * block barrier; 4 waves per 256-thread workgroup.
+ * reduces the statistic in double across its LPR lanes (DPP butterfly, no LDS,
+ * no barrier) and writes the transformed row once: HBM traffic = read x + write y.
+ * Broadcast vectors (w, b, scale, shift) are read as float4 at the same column.
  *
  * Statistics follow the reference: sum of squares accumulated in double
  * (src/aria_cpu.c:57-98), inv = (float)(1.0/sqrt(ss/dim + eps)), then the
  * per-element products in float with separate roundings. LayerNorm (which has
  * no reference op) keeps mean, variance and (x-mean)*rstd in double.
+ *
+ * The epilogue is a compile-time mask (EPI): modulate, GELU, residual, half output.
  */
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
+
+enum { EPI_MOD = 1, EPI_GELU = 2, EPI_RES = 4, EPI_F16 = 8 };
 
 struct NormArgs {
     void *y;
@@ -29,36 +33,36 @@ struct NormArgs {
 };
 
 template <int NORM>
-__device__ __forceinline__ float norm_elem(float xv, float inv, double mu, double rstd, const float *w,
-                                           const float *b, int c) {
+__device__ __forceinline__ float norm_elem(float xv, float inv, double mu, double rstd, bool hw, float w,
+                                           bool hb, float b) {
     float n;
     if (NORM == ARIA_NORM_LAYER) {
         n = (float)(((double)xv - mu) * rstd);
-        if (w) n = n * w[c];
-        if (b) n = n + b[c];
+        if (hw) n = n * w;
+        if (hb) n = n + b;
     } else if (NORM == ARIA_NORM_GEMMA) {
-        n = (xv * inv) * (1.0f + w[c]);
+        n = (xv * inv) * (1.0f + w);
     } else {
         n = xv * inv;
-        if (w) n = n * w[c];
+        if (hw) n = n * w;
     }
     return n;
 }
 
-__device__ __forceinline__ float epilogue(float n, float xv, const NormArgs &a, const float *sc,
-                                          const float *sh, int c) {
-    if (sc) {
-        float t = 1.0f + sc[c];
+template <int EPI>
+__device__ __forceinline__ float epi_elem(float n, float xv, float sc, float sh) {
+    if (EPI & EPI_MOD) {
+        float t = 1.0f + sc;
         n = n * t;
-        n = n + sh[c];
+        n = n + sh;
     }
-    if (a.gelu) n = gelu_tanh_f(n);
-    if (a.resid) n = n + xv;
+    if (EPI & EPI_GELU) n = gelu_tanh_f(n);
+    if (EPI & EPI_RES) n = n + xv;
     return n;
 }
 
 /* register-resident fast path: dim == VPL * 4 * LPR */
-template <int NORM, int VPL, int LPR>
+template <int NORM, int VPL, int LPR, int EPI>
 __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
     constexpr int RPW = ARIA_WAVE / LPR;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -100,29 +104,34 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
         inv = (float)(1.0 / sqrt(s / dim + (double)a.eps));
     }
 
-    const float *sc = nullptr, *sh = nullptr;
-    if (a.scale) {
-        int bt = row / a.rows_per_batch;
-        sc = a.scale + (size_t)bt * dim;
-        sh = a.shift + (size_t)bt * dim;
+    const float4 *w4 = reinterpret_cast<const float4 *>(a.w);
+    const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
+    const float4 *sc4 = nullptr, *sh4 = nullptr;
+    if (EPI & EPI_MOD) {
+        const int bt = row / a.rows_per_batch;
+        sc4 = reinterpret_cast<const float4 *>(a.scale + (size_t)bt * dim);
+        sh4 = reinterpret_cast<const float4 *>(a.shift + (size_t)bt * dim);
     }
+    const bool hw = a.w != nullptr, hb = a.b != nullptr;
 #pragma unroll
     for (int j = 0; j < VPL; j++) {
-        const int c0 = 4 * (j * LPR + l);
+        const int c4 = j * LPR + l;
+        const float4 wv = hw ? w4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 bv = hb ? b4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 scv = make_float4(0.f, 0.f, 0.f, 0.f), shv = scv;
+        if (EPI & EPI_MOD) { scv = sc4[c4]; shv = sh4[c4]; }
         float4 o;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            float xv = f4get(v[j], e);
-            float n = norm_elem<NORM>(xv, inv, mu, rstd, a.w, a.b, c0 + e);
-            f4set(o, e, epilogue(n, xv, a, sc, sh, c0 + e));
-        }
-        if (a.f16) {
+        o.x = epi_elem<EPI>(norm_elem<NORM>(v[j].x, inv, mu, rstd, hw, wv.x, hb, bv.x), v[j].x, scv.x, shv.x);
+        o.y = epi_elem<EPI>(norm_elem<NORM>(v[j].y, inv, mu, rstd, hw, wv.y, hb, bv.y), v[j].y, scv.y, shv.y);
+        o.z = epi_elem<EPI>(norm_elem<NORM>(v[j].z, inv, mu, rstd, hw, wv.z, hb, bv.z), v[j].z, scv.z, shv.z);
+        o.w = epi_elem<EPI>(norm_elem<NORM>(v[j].w, inv, mu, rstd, hw, wv.w, hb, bv.w), v[j].w, scv.w, shv.w);
+        if (EPI & EPI_F16) {
             uint2 p;
             p.x = (uint32_t)f2h_bits(o.x) | ((uint32_t)f2h_bits(o.y) << 16);
             p.y = (uint32_t)f2h_bits(o.z) | ((uint32_t)f2h_bits(o.w) << 16);
-            reinterpret_cast<uint2 *>((uint16_t *)a.y + (size_t)row * dim)[j * LPR + l] = p;
+            reinterpret_cast<uint2 *>((uint16_t *)a.y + (size_t)row * dim)[c4] = p;
         } else {
-            reinterpret_cast<float4 *>((float *)a.y + (size_t)row * dim)[j * LPR + l] = o;
+            reinterpret_cast<float4 *>((float *)a.y + (size_t)row * dim)[c4] = o;
         }
     }
 }
@@ -158,9 +167,13 @@ __global__ __launch_bounds__(256) void k_rownorm_g(NormArgs a) {
         sc = a.scale + (size_t)bt * dim;
         sh = a.shift + (size_t)bt * dim;
     }
+    const bool hw = a.w != nullptr, hb = a.b != nullptr;
     for (int c = lane; c < dim; c += 64) {
         float xv = xr[c];
-        float n = epilogue(norm_elem<NORM>(xv, inv, mu, rstd, a.w, a.b, c), xv, a, sc, sh, c);
+        float n = norm_elem<NORM>(xv, inv, mu, rstd, hw, hw ? a.w[c] : 0.0f, hb, hb ? a.b[c] : 0.0f);
+        if (sc) { float t = 1.0f + sc[c]; n = n * t; n = n + sh[c]; }
+        if (a.gelu) n = gelu_tanh_f(n);
+        if (a.resid) n = n + xv;
         if (a.f16) ((uint16_t *)a.y)[(size_t)row * dim + c] = f2h_bits(n);
         else ((float *)a.y)[(size_t)row * dim + c] = n;
     }
@@ -168,30 +181,46 @@ __global__ __launch_bounds__(256) void k_rownorm_g(NormArgs a) {
 
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+template <int NORM, int VPL, int LPR>
+static void launch_v(const NormArgs &a, int epi, hipStream_t s) {
+    constexpr int RPW = ARIA_WAVE / LPR;
+    dim3 grid((a.rows + 4 * RPW - 1) / (4 * RPW)), blk(256);
+    switch (epi) {
+        case 0: hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, 0>), grid, blk, 0, s, a); break;
+        case EPI_F16: hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, EPI_F16>), grid, blk, 0, s, a); break;
+        case EPI_MOD: hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, EPI_MOD>), grid, blk, 0, s, a); break;
+        case EPI_MOD | EPI_F16:
+            hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, EPI_MOD | EPI_F16>), grid, blk, 0, s, a); break;
+        case EPI_MOD | EPI_GELU | EPI_RES:
+            hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, EPI_MOD | EPI_GELU | EPI_RES>), grid, blk, 0, s, a);
+            break;
+        default: hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), blk, 0, s, a); break;
+    }
+}
+
 template <int NORM>
 static hipError_t launch_norm(const NormArgs &a, hipStream_t s) {
     const int dim = a.dim;
-    bool vec = (dim % 4 == 0) && al16(a.x) && (a.f16 ? ((uintptr_t)a.y & 7u) == 0 : al16(a.y)) &&
-               (!a.w || al16(a.w)) && (!a.b || al16(a.b)) && (!a.scale || al16(a.scale)) &&
-               (!a.shift || al16(a.shift));
-    dim3 blk(256);
-    auto grid_for = [&](int rows_per_wave) { return dim3((a.rows + 4 * rows_per_wave - 1) / (4 * rows_per_wave)); };
-    if (vec && dim == 64) {
-        hipLaunchKernelGGL((k_rownorm_v<NORM, 1, 16>), grid_for(4), blk, 0, s, a);
-    } else if (vec && dim == 128) {
-        hipLaunchKernelGGL((k_rownorm_v<NORM, 1, 32>), grid_for(2), blk, 0, s, a);
-    } else if (vec && dim == 256) {
-        hipLaunchKernelGGL((k_rownorm_v<NORM, 1, 64>), grid_for(1), blk, 0, s, a);
-    } else if (vec && dim == 512) {
-        hipLaunchKernelGGL((k_rownorm_v<NORM, 2, 64>), grid_for(1), blk, 0, s, a);
-    } else if (vec && dim == 768) {
-        hipLaunchKernelGGL((k_rownorm_v<NORM, 3, 64>), grid_for(1), blk, 0, s, a);
-    } else if (vec && dim == 1024) {
-        hipLaunchKernelGGL((k_rownorm_v<NORM, 4, 64>), grid_for(1), blk, 0, s, a);
-    } else if (vec && dim == 2048) {
-        hipLaunchKernelGGL((k_rownorm_v<NORM, 8, 64>), grid_for(1), blk, 0, s, a);
-    } else {
-        hipLaunchKernelGGL((k_rownorm_g<NORM>), grid_for(1), blk, 0, s, a);
+    const bool vec = (dim % 4 == 0) && al16(a.x) && (a.f16 ? ((uintptr_t)a.y & 7u) == 0 : al16(a.y)) &&
+                     (!a.w || al16(a.w)) && (!a.b || al16(a.b)) && (!a.scale || al16(a.scale)) &&
+                     (!a.shift || al16(a.shift));
+    int epi = (a.scale ? EPI_MOD : 0) | (a.gelu ? EPI_GELU : 0) | (a.resid ? EPI_RES : 0) | (a.f16 ? EPI_F16 : 0);
+    /* only these epilogues are instantiated for the register path; others take the generic kernel */
+    const bool known = epi == 0 || epi == EPI_F16 || epi == EPI_MOD || epi == (EPI_MOD | EPI_F16) ||
+                       epi == (EPI_MOD | EPI_GELU | EPI_RES);
+    if (!vec || !known) {
+        hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
+    switch (dim) {
+        case 64: launch_v<NORM, 1, 16>(a, epi, s); break;
+        case 128: launch_v<NORM, 1, 32>(a, epi, s); break;
+        case 256: launch_v<NORM, 1, 64>(a, epi, s); break;
+        case 512: launch_v<NORM, 2, 64>(a, epi, s); break;
+        case 768: launch_v<NORM, 3, 64>(a, epi, s); break;
+        case 1024: launch_v<NORM, 4, 64>(a, epi, s); break;
+        case 2048: launch_v<NORM, 8, 64>(a, epi, s); break;
+        default: hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), dim3(256), 0, s, a); break;
     }
     return hipGetLastError();
 }

@@ -6,7 +6,11 @@
  *   v = x + mask; m = max v; e = expf(v - m); s = sum e;
  *   inv = s > 0 ? 1/s : 0; x = e * inv.
  * The reference sums e sequentially; here each lane sums its share and a
- * wave64 butterfly finishes, which stays inside the 1e-5 gate.
+ * wave64 butterfly finishes, which stays inside the 1e-5 gate. exp(v - m) is
+ * computed as 2^((v - m)*log2e) with v_exp_f32 (relative error ~|v-m| * 4e-8),
+ * so the kernel stays bandwidth-bound; v - m is formed first, as in the
+ * reference, so rows masked with -3.4e38 stay finite. The score tensor is
+ * streamed once, so loads and stores are non-temporal.
  *
  * Mapping: one wave64 per row, the row held in registers (NV float4 per lane,
  * lane l owns vectors l, l+64, ...), so the row is read once and written once:
@@ -30,7 +34,7 @@ __global__ __launch_bounds__(256) void k_softmax_v(float *x, int rows, int cols,
     for (int j = 0; j < NV; j++) {
         const int idx = j * 64 + lane;
         if (idx < n4) {
-            v[j] = xr[idx];
+            v[j] = ld_nt(xr + idx);
             if (mr) {
                 float4 k = mr[idx];
                 v[j].x += k.x; v[j].y += k.y; v[j].z += k.z; v[j].w += k.w;
@@ -44,8 +48,10 @@ __global__ __launch_bounds__(256) void k_softmax_v(float *x, int rows, int cols,
     for (int j = 0; j < NV; j++) {
         const int idx = j * 64 + lane;
         if (idx < n4) {
-            v[j].x = expf(v[j].x - m); v[j].y = expf(v[j].y - m);
-            v[j].z = expf(v[j].z - m); v[j].w = expf(v[j].w - m);
+            v[j].x = __builtin_amdgcn_exp2f((v[j].x - m) * ARIA_LOG2E);
+            v[j].y = __builtin_amdgcn_exp2f((v[j].y - m) * ARIA_LOG2E);
+            v[j].z = __builtin_amdgcn_exp2f((v[j].z - m) * ARIA_LOG2E);
+            v[j].w = __builtin_amdgcn_exp2f((v[j].w - m) * ARIA_LOG2E);
             s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
         }
     }
@@ -57,7 +63,7 @@ __global__ __launch_bounds__(256) void k_softmax_v(float *x, int rows, int cols,
         if (idx < n4) {
             float4 o = v[j];
             o.x *= inv; o.y *= inv; o.z *= inv; o.w *= inv;
-            xr[idx] = o;
+            st_nt(xr + idx, o);
         }
     }
 }

@@ -58,6 +58,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (cache defeat)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--pmc-mode", action="store_true",
+                    help="for rocprofv3 --pmc: each C2 op a few times with no events in between, plus one "
+                         "256 MiB device-to-device copy whose FETCH/WRITE counters calibrate the others")
     return ap.parse_args()
 
 
@@ -182,8 +185,7 @@ def main():
         if name == "ln":
             return L.aria_hip_layernorm_dev(st["y2"].p, st["x"].p, None, None, rows, D, 1e-6, stream)
         if name == "rope":
-            rc = L.aria_hip_rope_apply_dev(st["q"].p, d_cos.p, d_sin.p, B * H, S, HD, 64, stream)
-            return rc or L.aria_hip_rope_apply_dev(st["k"].p, d_cos.p, d_sin.p, B * H, S, HD, 64, stream)
+            return L.aria_hip_rope_apply2_dev(st["q"].p, st["k"].p, d_cos.p, d_sin.p, B * H, S, HD, 64, stream)
         if name == "softmax":
             return L.aria_hip_softmax_dev(st["s"].p, B * H * S, S, None, stream)
         raise KeyError(name)
@@ -191,6 +193,17 @@ def main():
     OPS = ["chain", "rms", "ln", "rope", "softmax"]
     ab = algorithmic_bytes()
     step_bytes = sum(ab.values())
+
+    if args.pmc_mode:
+        for i in range(3):
+            for op in OPS:
+                chk(run_op(op, sets[i % len(sets)]), op)
+        cal = 256 << 20
+        a, b = DeviceArray(cal // 4), DeviceArray(cal // 4)
+        chk(L.aria_hip_memcpy_d2d_async(b.p, a.p, cal, stream))
+        chk(L.aria_hip_stream_sync(stream))
+        print(json.dumps({"pmc_mode": True, "copy_bytes": cal, "algorithmic_bytes": ab}), flush=True)
+        return
 
     for i in range(args.warmup):
         for op in OPS:
@@ -237,8 +250,7 @@ def main():
     tm.start()
     for i in range(reps):
         s_ = sets[i % len(sets)]
-        chk(L.aria_hip_rope_apply_dev(s_["q"].p, d_cos.p, d_sin.p, B * H, S, HD, 32, stream))
-        chk(L.aria_hip_rope_apply_dev(s_["k"].p, d_cos.p, d_sin.p, B * H, S, HD, 32, stream))
+        chk(L.aria_hip_rope_apply2_dev(s_["q"].p, s_["k"].p, d_cos.p, d_sin.p, B * H, S, HD, 32, stream))
     ms = tm.stop() / reps
     rope32_bytes = 2 * 2 * B * H * S * 32 * 4 + 2 * S * 16 * 4
     ops_report["rope_rot32"] = {"us": round(ms * 1e3, 2), "GB/s": round(rope32_bytes / (ms * 1e-3) / 1e9, 1),

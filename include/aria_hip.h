@@ -111,6 +111,10 @@ int aria_hip_softmax_dev(float *dx, int rows, int cols, const float *dmask, void
 /* aria_rope_apply (src/aria_ops.h:126): x [H, N, D] in place, tables [N, rot/2]. */
 int aria_hip_rope_apply_dev(float *dx, const float *dcos, const float *dsin, int H, int N, int D,
                             int rot_dim, void *stream);
+/* The same rotation on q and k (same shape, distinct buffers) in one launch, as the
+ * DiT applies it (src/aria_sa3_dit.c:193-194). */
+int aria_hip_rope_apply2_dev(float *dq, float *dk, const float *dcos, const float *dsin, int H, int N,
+                             int D, int rot_dim, void *stream);
 
 /* ---- quantisation (src/aria_quant.h layouts) ---- */
 /* Device pack: bit-exact with aria_q8_quant / aria_q4_quant (src/aria_quant.c:78, 353). */

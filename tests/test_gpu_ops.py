@@ -265,3 +265,28 @@ def test_argument_errors(hip):
     assert L.aria_hip_rmsnorm_adaln_dev(None, 0, None, None, None, None, 4, 8, 3, 1e-5, None) == -1
     assert L.aria_hip_rope_apply_dev(None, None, None, 1, 1, 8, 10, None) == -1
     assert "invalid argument" in hip.last_error()
+
+
+def test_rope_two_tensors_one_launch(hip, port):
+    """aria_hip_rope_apply2_dev rotates q and k exactly as two single-tensor calls."""
+    from aria_amd.device import DeviceArray, sync
+    r = rng(41)
+    for rot in (32, 64, 6):
+        H, N, D = 8, 100, 64
+        c, s = port.rope_freqs(N, rot, 10000.0)
+        q = randn(r, (H, N, D)); k = randn(r, (H, N, D))
+        dq, dk, dc, ds = (DeviceArray.from_host(a) for a in (q, k, c, s))
+        hip.check(hip.lib().aria_hip_rope_apply2_dev(dq.p, dk.p, dc.p, ds.p, H, N, D, rot, None))
+        sync()
+        assert_close(dq.to_host(), port.rope_apply(q, c, s, rot), 1e-5, 1e-5, f"q rot {rot}")
+        assert_close(dk.to_host(), port.rope_apply(k, c, s, rot), 1e-5, 1e-5, f"k rot {rot}")
+
+
+def test_softmax_fully_masked_rows(ops, port):
+    """Rows whose every column carries the -3.4e38 padding mask stay finite, as in the reference."""
+    r = rng(42)
+    s = randn(r, (8, 1296), 2.0)
+    m = np.full_like(s, -3.4e38)
+    got = ops.softmax(s, m)
+    assert np.all(np.isfinite(got))
+    assert_close(got, port.softmax(s, m), 1e-5, 1e-5, "all-masked")
