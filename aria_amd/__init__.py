@@ -90,7 +90,13 @@ SIGNATURES = {
     "aria_hip_q4_quant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
     "aria_hip_q8_dequant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
     "aria_hip_q4_dequant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
+    "aria_hip_qlinear_dev": (_i, [_P, _i, _P, _i, _i, _P, _P, _P, _i, _i, _i, _P]),
+    "aria_hip_qlinear_ex_dev": (_i, [_P, _i, _P, _i, _i, _P, _P, _P, _i, _i, _i, _i, _P]),
+    "aria_hip_linear_q8_dev": (_i, [_P, _P, _P, _P, _P, _i, _i, _i, _P]),
+    "aria_hip_linear_q4_dev": (_i, [_P, _P, _P, _P, _P, _i, _i, _i, _P]),
     # include/aria_hip.h: host-pointer forms
+    "aria_hip_linear_q8": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
+    "aria_hip_linear_q4": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
     "aria_hip_q8_quant": (_i, [_P, _P, _P, _i, _i]),
     "aria_hip_q4_quant": (_i, [_P, _P, _P, _i, _i]),
     "aria_hip_q8_dequant": (_i, [_P, _P, _P, _i, _i]),

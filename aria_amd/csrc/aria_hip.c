@@ -432,12 +432,77 @@ int aria_hip_q4_dequant_dev(float *dW, const uint8_t *dq, const float *dscale, i
     return 0;
 }
 
+int aria_hip_qlinear_ex_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
+                            const float *dscale, const float *db, int M, int K, int N, int tiles, void *stream) {
+    ENSURE();
+    REQ(M >= 0 && K > 0 && N >= 0 && tiles >= 0 && tiles <= 4);
+    REQ(wtype == ARIA_WQ8 || wtype == ARIA_WQ4 || wtype == ARIA_WF16);
+    REQ(M == 0 || N == 0 || (dy && dx && dq && (wtype == ARIA_WF16 || dscale)));
+    if (M == 0 || N == 0) return 0;
+    hipStream_t s = pick(stream);
+    /* fp32 activations: one conversion pass to fp16 (stream-ordered pool memory), then the
+     * fp16-operand kernel, which stages half the bytes per slice; the value rounded is the
+     * same RTNE half the in-kernel staging would produce */
+    void *x16 = NULL;
+    if (!x_f16 && K % 32 == 0 && ((uintptr_t)dx & 15u) == 0 &&
+        hipMallocAsync(&x16, (size_t)M * K * 2, s) == hipSuccess) {
+        hipError_t e = aria_k_f32_to_f16((uint16_t *)x16, (const float *)dx, (size_t)M * K, s);
+        if (e == hipSuccess) e = aria_k_qgemm_t(dy, y_f16, x16, 1, wtype, dq, dscale, db, M, K, N, tiles, s);
+        hipError_t ef = hipFreeAsync(x16, s);
+        if (e == hipSuccess) e = ef;
+        KCK(e, "k_qgemm (fp16-staged activations)");
+        return 0;
+    }
+    hipGetLastError();   /* a refused pool allocation leaves no sticky error: take the direct path */
+    KCK(aria_k_qgemm_t(dy, y_f16, dx, x_f16, wtype, dq, dscale, db, M, K, N, tiles, s), "k_qgemm");
+    return 0;
+}
+int aria_hip_qlinear_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
+                         const float *dscale, const float *db, int M, int K, int N, void *stream) {
+    return aria_hip_qlinear_ex_dev(dy, y_f16, dx, x_f16, wtype, dq, dscale, db, M, K, N, 0, stream);
+}
+int aria_hip_linear_q8_dev(float *dy, const float *dx, const int8_t *dq, const float *dscale, const float *db,
+                           int M, int K, int N, void *stream) {
+    return aria_hip_qlinear_dev(dy, 0, dx, 0, ARIA_WQ8, dq, dscale, db, M, K, N, stream);
+}
+int aria_hip_linear_q4_dev(float *dy, const float *dx, const uint8_t *dq, const float *dscale, const float *db,
+                           int M, int K, int N, void *stream) {
+    return aria_hip_qlinear_dev(dy, 0, dx, 0, ARIA_WQ4, dq, dscale, db, M, K, N, stream);
+}
+
 /* ------------------------------------------------------------------------- */
 /* host-pointer forms (aria_hip.h) - one synchronous staged call each        */
 /* ------------------------------------------------------------------------- */
 
 #define HOST_BEGIN() stage_t st_ = {{0}, 0, 0}; ENSURE()
 #define HOST_END() return st_finish(&st_)
+
+static int host_qlinear(float *y, const float *x, int wtype, const void *q, const float *scale, const float *b,
+                        int M, int K, int N) {
+    HOST_BEGIN();
+    REQ(M >= 0 && K > 0 && N >= 0 && y && x && q && scale);
+    if (M == 0 || N == 0) return 0;
+    size_t qb = wtype == ARIA_WQ8 ? (size_t)N * K : (size_t)N * ((K + 1) / 2);
+    size_t ns = wtype == ARIA_WQ8 ? (size_t)N : (size_t)N * 2 * ((K + 31) / 32);
+    float *dx = st_in(&st_, x, FB((size_t)M * K));
+    void *dq = st_in(&st_, q, qb);
+    float *ds = st_in(&st_, scale, FB(ns));
+    float *db = st_in(&st_, b, FB(N));
+    float *dy = st_alloc(&st_, FB((size_t)M * N));
+    if (!st_.err)
+        st_.err = aria_hip_qlinear_dev(dy, 0, dx, 0, wtype, dq, ds, db, M, K, N, g_stream);
+    st_out(&st_, y, dy, FB((size_t)M * N));
+    HOST_END();
+}
+int aria_hip_linear_q8(float *y, const float *x, const int8_t *q, const float *scale, const float *b, int M,
+                       int K, int N) {
+    return host_qlinear(y, x, ARIA_WQ8, q, scale, b, M, K, N);
+}
+int aria_hip_linear_q4(float *y, const float *x, const uint8_t *q, const float *scale, const float *b, int M,
+                       int K, int N) {
+    return host_qlinear(y, x, ARIA_WQ4, q, scale, b, M, K, N);
+}
+
 
 int aria_hip_q8_quant(int8_t *q, float *scale, const float *W, int N, int K) {
     HOST_BEGIN();

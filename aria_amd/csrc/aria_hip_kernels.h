@@ -75,6 +75,19 @@ hipError_t aria_k_q8_dequant(float *W, const int8_t *q, const float *scale, int 
 hipError_t aria_k_q4_dequant(float *W, const uint8_t *q, const float *scale, int N, int K,
                              hipStream_t s);
 
+/* Dequant-on-use GEMM on MFMA (k_qgemm.hip): y[M,N] = x[M,K] W^T (+ bias[N]).
+ * wtype: ARIA_WQ8 (q int8 [N,K], scale [N]), ARIA_WQ4 (q u8 [N,ceil(K/2)], scale
+ * [N, 2*ceil(K/32)] as [min, step] pairs), ARIA_WF16 (q = fp16 W [N,K], scale unused).
+ * x is fp32 or fp16 (x_f16), y fp32 or fp16 (y_f16). */
+enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2 };
+hipError_t aria_k_qgemm(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
+                        const float *scale, const float *bias, int M, int K, int N, hipStream_t s);
+/* the same with an explicit workgroup tile: 1 = 128x128, 2 = 128x64, 3 = 64x128,
+ * 4 = 64x64 (M x N); 0 = picked from the shape */
+hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
+                          const float *scale, const float *bias, int M, int K, int N, int tiles,
+                          hipStream_t s);
+
 /* fp32 SIMT GEMM (k_sgemm.hip), batched with element strides sA/sB/sC:
  * C_b[M,N] = alpha * (A_b[M,K] op(B_b)) (+ bias[N]); op(B) = B^T for B_b [N,K]
  * (transB = 1, Linear layout) or B for B_b [K,N] (transB = 0). */

@@ -292,11 +292,21 @@ extern "C" hipError_t aria_k_pingpong(float *x, const float *v, const float *noi
 }
 
 /* fp32 -> fp16 RTNE (the reference's k_f32_to_f16 / aria_f32_to_f16_n) */
+__global__ __launch_bounds__(256) void k_f2h4(uint2 *y, const float4 *x, size_t n4) {
+    GRID_STRIDE(i, n4) {
+        const float4 v = x[i];
+        y[i] = make_uint2((uint32_t)f2h_bits(v.x) | ((uint32_t)f2h_bits(v.y) << 16),
+                          (uint32_t)f2h_bits(v.z) | ((uint32_t)f2h_bits(v.w) << 16));
+    }
+}
 __global__ __launch_bounds__(256) void k_f2h(uint16_t *y, const float *x, size_t n) {
     GRID_STRIDE(i, n) y[i] = f2h_bits(x[i]);
 }
 extern "C" hipError_t aria_k_f32_to_f16(uint16_t *y, const float *x, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_f2h, stream_grid((n + 3) / 4), dim3(256), 0, s, y, x, n);
+    if (n % 4 == 0 && al16(x) && ((uintptr_t)y & 7u) == 0)
+        hipLaunchKernelGGL(k_f2h4, stream_grid(n / 4), dim3(256), 0, s, (uint2 *)y, (const float4 *)x, n / 4);
+    else
+        hipLaunchKernelGGL(k_f2h, stream_grid((n + 3) / 4), dim3(256), 0, s, y, x, n);
     return hipGetLastError();
 }

@@ -214,6 +214,28 @@ def q4_quant(W):
     return q, s
 
 
+def linear_q8(x, q, s, b=None):
+    """aria_linear_q8 (src/aria_quant.h:45): y = x dequant(q, s)^T + b, on MFMA."""
+    x = _f32(x); b = _f32(b)
+    M, K = x.shape
+    N = q.shape[0]
+    y = np.empty((M, N), np.float32)
+    check(lib().aria_hip_linear_q8(_p(y), _p(x), _p(np.ascontiguousarray(q)), _p(np.ascontiguousarray(s)),
+                                   _p(b), M, K, N), "aria_hip_linear_q8")
+    return y
+
+
+def linear_q4(x, q, s, b=None):
+    """aria_linear_q4 (src/aria_quant.h:65): y = x dequant(q, s)^T + b, on MFMA."""
+    x = _f32(x); b = _f32(b)
+    M, K = x.shape
+    N = q.shape[0]
+    y = np.empty((M, N), np.float32)
+    check(lib().aria_hip_linear_q4(_p(y), _p(x), _p(np.ascontiguousarray(q)), _p(np.ascontiguousarray(s)),
+                                   _p(b), M, K, N), "aria_hip_linear_q4")
+    return y
+
+
 def q8_dequant(q, s):
     N, K = q.shape
     W = np.empty((N, K), np.float32)

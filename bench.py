@@ -31,6 +31,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, AMD published
+FP16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 MFMA, AMD published
 B, S, D, H, HD = 2, 1296, 1024, 16, 64
 SEED = 0xA21A0000
 
@@ -210,48 +211,41 @@ def main():
             chk(run_op(op, sets[i % len(sets)]), op)
     chk(L.aria_hip_stream_sync(stream))
 
-    # timed region: events between consecutive kernels on the launch stream
-    nev = args.steps * len(OPS) + 1
-    evs = [L.aria_hip_event_create() for _ in range(nev)]
+    def time_loop(fn, reps):
+        """average ms of fn(i) over reps back-to-back launches, HIP events on the launch stream"""
+        tm = Timer(stream)
+        chk(fn(0))                          # first launch loads the code object
+        chk(L.aria_hip_stream_sync(stream))
+        tm.start()
+        for i in range(reps):
+            chk(fn(i))
+        return tm.stop() / reps
+
+    # timed region (value): K whole steps, events only around them
+    tmr = Timer(stream)
     chk(L.aria_hip_stream_sync(stream))
     t_wall0 = time.perf_counter()
-    e = 0
-    chk(L.aria_hip_event_record(evs[e], stream))
+    tmr.start()
     for i in range(args.steps):
         st = sets[i % len(sets)]
         for op in OPS:
             chk(run_op(op, st), op)
-            e += 1
-            chk(L.aria_hip_event_record(evs[e], stream))
-    chk(L.aria_hip_stream_sync(stream))
+    total_ms = tmr.stop()
     t_wall = time.perf_counter() - t_wall0
-    per_op = {op: [] for op in OPS}
-    e = 0
-    for i in range(args.steps):
-        for op in OPS:
-            per_op[op].append(L.aria_hip_event_elapsed_ms(evs[e], evs[e + 1]))
-            e += 1
-    total_ms = L.aria_hip_event_elapsed_ms(evs[0], evs[-1])
-    for ev in evs:
-        L.aria_hip_event_destroy(ev)
     ms_per_step = total_ms / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
+    # per-op average launch duration: each op back to back over the rotating sets
+    reps = max(args.steps, 20)
     ops_report = {}
     for op in OPS:
-        avg = float(np.mean(per_op[op]))
+        avg = time_loop(lambda i, op=op: run_op(op, sets[i % len(sets)]), reps)
         ops_report[op] = {"us": round(avg * 1e3, 2), "GB/s": round(ab[op] / (avg * 1e-3) / 1e9, 1),
                           "bytes": ab[op], "frac_peak": round(ab[op] / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
 
     # extra: rot-32 RoPE (the DiT's), Q8/Q4 pack of W [4096, 1024]
-    tm = Timer(stream)
-    st = sets[0]
-    reps = 20
-    tm.start()
-    for i in range(reps):
-        s_ = sets[i % len(sets)]
-        chk(L.aria_hip_rope_apply2_dev(s_["q"].p, s_["k"].p, d_cos.p, d_sin.p, B * H, S, HD, 32, stream))
-    ms = tm.stop() / reps
+    ms = time_loop(lambda i: L.aria_hip_rope_apply2_dev(sets[i % len(sets)]["q"].p, sets[i % len(sets)]["k"].p,
+                                                        d_cos.p, d_sin.p, B * H, S, HD, 32, stream), reps)
     rope32_bytes = 2 * 2 * B * H * S * 32 * 4 + 2 * S * 16 * 4
     ops_report["rope_rot32"] = {"us": round(ms * 1e3, 2), "GB/s": round(rope32_bytes / (ms * 1e-3) / 1e9, 1),
                                 "bytes": rope32_bytes}
@@ -263,13 +257,13 @@ def main():
     for name, fn, outb in (("q8_pack", L.aria_hip_q8_quant_dev, Wn * Wk + Wn * 4),
                            ("q4_pack", L.aria_hip_q4_quant_dev, Wn * Wk // 2 + Wn * 2 * (Wk // 32) * 4)):
         dq, ds = (d_q8, d_s8) if name == "q8_pack" else (d_q4, d_s4)
-        chk(fn(dq.p, ds.p, d_W[0].p, Wn, Wk, stream))
-        tm.start()
-        for i in range(reps):
-            chk(fn(dq.p, ds.p, d_W[i % 8].p, Wn, Wk, stream))
-        ms = tm.stop() / reps
+        ms = time_loop(lambda i, fn=fn, dq=dq, ds=ds: fn(dq.p, ds.p, d_W[i % 8].p, Wn, Wk, stream), reps)
         byt = Wn * Wk * 4 + outb
         ops_report[name] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / (ms * 1e-3) / 1e9, 1), "bytes": byt}
+    del d_W
+
+    # C3: Q8 / Q4 dequant-on-use GEMMs at M = 2592 (fp32 activations, as aria_linear_q8/q4 take)
+    gemm = gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps)
 
     dom = max(OPS, key=lambda o: ops_report[o]["us"])
     dom_us = ops_report[dom]["us"]
@@ -299,10 +293,39 @@ def main():
                      "algorithmic_bytes": ab[dom], "avg_us": dom_us},
         "cpu_baseline": cpu,
         "ops": ops_report,
+        "gemm": gemm,
         "block_us": None,
         "wall_s_timed": round(t_wall, 3),
     }
     print(json.dumps(line), flush=True)
+
+
+def gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps):
+    """Config 3: X [2592,K] ~N(0,1) times W [N,K] ~N(0,0.02) packed on the device (bit-exact with
+    the reference quantizer), for (K,N) = (1024,4096) and (4096,1024), Q8 and Q4."""
+    out = {}
+    M = B * S
+    for K, N in ((1024, 4096), (4096, 1024)):
+        Wh = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+        dW = DeviceArray.from_host(Wh)
+        dx = [DeviceArray.from_host(rng.standard_normal((M, K), dtype=np.float32)) for _ in range(2)]
+        dy = DeviceArray((M, N))
+        dq8, ds8 = DeviceArray((N, K), np.int8), DeviceArray(N, np.float32)
+        dq4, ds4 = DeviceArray((N, K // 2), np.uint8), DeviceArray((N, 2 * K // 32), np.float32)
+        chk(L.aria_hip_q8_quant_dev(dq8.p, ds8.p, dW.p, N, K, stream))
+        chk(L.aria_hip_q4_quant_dev(dq4.p, ds4.p, dW.p, N, K, stream))
+        flop = 2.0 * M * N * K
+        for wt, (dq, ds) in ((0, (dq8, ds8)), (1, (dq4, ds4))):
+            fn = (lambda i, dq=dq, ds=ds, wt=wt: L.aria_hip_qlinear_dev(dy.p, 0, dx[i % 2].p, 0, wt, dq.p, ds.p,
+                                                                        None, M, K, N, stream))
+            for i in range(3):
+                chk(fn(i))
+            ms = time_loop(fn, reps)
+            tf = flop / (ms * 1e-3) / 1e12
+            key = f"{'q8' if wt == 0 else 'q4'}_M{M}_K{K}_N{N}"
+            out[key] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                        "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 3), "flop": flop}
+    return out
 
 
 def _pmc_traffic(kernel_key):

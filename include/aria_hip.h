@@ -126,12 +126,35 @@ int aria_hip_q8_dequant_dev(float *dW, const int8_t *dq, const float *dscale, in
 int aria_hip_q4_dequant_dev(float *dW, const uint8_t *dq, const float *dscale, int N, int K,
                             void *stream);
 
-/* Host-pointer forms with the reference's signatures (src/aria_quant.h:43, 64):
+/* Dequant-on-use GEMM on MFMA, y[M,N] = x[M,K] W[N,K]^T (+ b[N]); b may be NULL.
+ * Replaces aria_linear_q8 / aria_linear_q4 (src/aria_quant.h:45, 65;
+ * src/aria_quant.c:98-145, 469-538) and the reference's dequantize-to-fp16 +
+ * cublasGemmEx device path (src/aria_cuda.cu:1009-1035). Weights stay packed in HBM.
+ * wtype 0 = Q8 (dq int8 [N,K], dscale [N]), 1 = Q4 (dq u8 [N,ceil(K/2)], dscale
+ * [N, 2*ceil(K/32)] [min,step] pairs), 2 = fp16 weights (dq = half [N,K], dscale unused).
+ * x_f16 / y_f16 select IEEE-half activations / outputs instead of fp32. */
+int aria_hip_qlinear_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
+                         const float *dscale, const float *db, int M, int K, int N, void *stream);
+/* As aria_hip_qlinear_dev with an explicit workgroup tile (M x N): 1 = 128x128,
+ * 2 = 128x64, 3 = 64x128, 4 = 64x64, 0 = chosen from the shape (tuning knob). */
+int aria_hip_qlinear_ex_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
+                            const float *dscale, const float *db, int M, int K, int N, int tiles,
+                            void *stream);
+int aria_hip_linear_q8_dev(float *dy, const float *dx, const int8_t *dq, const float *dscale,
+                           const float *db, int M, int K, int N, void *stream);
+int aria_hip_linear_q4_dev(float *dy, const float *dx, const uint8_t *dq, const float *dscale,
+                           const float *db, int M, int K, int N, void *stream);
+
+/* Host-pointer forms with the reference's signatures (src/aria_quant.h:43-45, 64-65):
  * allocate, copy in, run, copy out, free; synchronous. Return 0 or an error. */
 int aria_hip_q8_quant(int8_t *q, float *scale, const float *W, int N, int K);
 int aria_hip_q4_quant(uint8_t *q, float *scale, const float *W, int N, int K);
 int aria_hip_q8_dequant(float *W, const int8_t *q, const float *scale, int N, int K);
 int aria_hip_q4_dequant(float *W, const uint8_t *q, const float *scale, int N, int K);
+int aria_hip_linear_q8(float *y, const float *x, const int8_t *q, const float *scale,
+                       const float *b, int M, int K, int N);
+int aria_hip_linear_q4(float *y, const float *x, const uint8_t *q, const float *scale,
+                       const float *b, int M, int K, int N);
 
 /* ---- host-pointer forms of the fused ops (parity entry points) ---- */
 int aria_hip_layernorm(float *y, const float *x, const float *gamma, const float *beta,
