@@ -94,6 +94,9 @@ SIGNATURES = {
     "aria_hip_qlinear_ex_dev": (_i, [_P, _i, _P, _i, _i, _P, _P, _P, _i, _i, _i, _i, _P]),
     "aria_hip_linear_q8_dev": (_i, [_P, _P, _P, _P, _P, _i, _i, _i, _P]),
     "aria_hip_linear_q4_dev": (_i, [_P, _P, _P, _P, _P, _i, _i, _i, _P]),
+    "aria_hip_qkv_prep_dev": (_i, [_P, _i, _i, _i, _i, _i, _P, _P, _P, _P, _P, _i, _f, _P]),
+    "aria_hip_flash_attention_dev": (_i, [_P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _P]),
+    "aria_hip_attention_f16": (_i, [_P, _P, _P, _P, _i, _i, _i, _i, _i]),
     # include/aria_hip.h: host-pointer forms
     "aria_hip_linear_q8": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
     "aria_hip_linear_q4": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),

@@ -461,6 +461,30 @@ int aria_hip_qlinear_dev(void *dy, int y_f16, const void *dx, int x_f16, int wty
                          const float *dscale, const float *db, int M, int K, int N, void *stream) {
     return aria_hip_qlinear_ex_dev(dy, y_f16, dx, x_f16, wtype, dq, dscale, db, M, K, N, 0, stream);
 }
+int aria_hip_qkv_prep_dev(const float *dsrc, int ld, int B, int S, int H, int nsec, const int *kind,
+                          uint16_t *const *ddst, const float *const *dw, const float *dcos, const float *dsin,
+                          int rot, float eps, void *stream) {
+    ENSURE();
+    REQ(B >= 0 && S >= 0 && H > 0 && nsec >= 1 && nsec <= 3 && kind && ddst);
+    REQ(ld >= nsec * H * 64 && ld % 4 == 0 && (rot == 0 || rot == 32 || rot == 64));
+    REQ(B == 0 || S == 0 || (dsrc && ((uintptr_t)dsrc & 15u) == 0));
+    for (int i = 0; i < nsec; i++) {
+        REQ(kind[i] >= 0 && kind[i] <= 2 && ddst[i] && ((uintptr_t)ddst[i] & 7u) == 0);
+        if (kind[i] != 2 && rot) REQ(dcos && dsin);
+    }
+    KCK(aria_k_qkv_prep(dsrc, ld, B, S, H, nsec, kind, ddst, dw, dcos, dsin, rot, eps, pick(stream)),
+        "k_qkv_prep");
+    return 0;
+}
+int aria_hip_flash_attention_dev(const uint16_t *dq, const uint16_t *dk, const uint16_t *dv, void *dout,
+                                 int out_f16, int B, int H, int Nq, int Nk, int D, void *stream) {
+    ENSURE();
+    REQ(D == 64 && B >= 0 && H > 0 && Nq >= 0 && Nk > 0);
+    REQ(B == 0 || Nq == 0 || (dq && dk && dv && dout));
+    REQ((((uintptr_t)dq | (uintptr_t)dk | (uintptr_t)dv) & 15u) == 0 && ((uintptr_t)dout & 15u) == 0);
+    KCK(aria_k_flash_attn(dq, dk, dv, dout, out_f16, B * H, H, Nq, Nk, pick(stream)), "k_flash_attn");
+    return 0;
+}
 int aria_hip_linear_q8_dev(float *dy, const float *dx, const int8_t *dq, const float *dscale, const float *db,
                            int M, int K, int N, void *stream) {
     return aria_hip_qlinear_dev(dy, 0, dx, 0, ARIA_WQ8, dq, dscale, db, M, K, N, stream);
@@ -492,6 +516,23 @@ static int host_qlinear(float *y, const float *x, int wtype, const void *q, cons
     if (!st_.err)
         st_.err = aria_hip_qlinear_dev(dy, 0, dx, 0, wtype, dq, ds, db, M, K, N, g_stream);
     st_out(&st_, y, dy, FB((size_t)M * N));
+    HOST_END();
+}
+int aria_hip_attention_f16(float *out, const float *q, const float *k, const float *v, int B, int H, int Nq,
+                           int Nk, int D) {
+    HOST_BEGIN();
+    REQ(out && q && k && v && B > 0 && H > 0 && Nq > 0 && Nk > 0 && D == 64);
+    size_t nq = (size_t)B * H * Nq * D, nk = (size_t)B * H * Nk * D;
+    float *dq32 = st_in(&st_, q, FB(nq));
+    float *dk32 = st_in(&st_, k, FB(nk));
+    float *dv32 = st_in(&st_, v, FB(nk));
+    uint16_t *dq = st_alloc(&st_, nq * 2), *dk = st_alloc(&st_, nk * 2), *dv = st_alloc(&st_, nk * 2);
+    float *dout = st_alloc(&st_, FB(nq));
+    if (!st_.err) st_kernel(&st_, aria_k_f32_to_f16(dq, dq32, nq, g_stream), "k_f2h");
+    if (!st_.err) st_kernel(&st_, aria_k_f32_to_f16(dk, dk32, nk, g_stream), "k_f2h");
+    if (!st_.err) st_kernel(&st_, aria_k_f32_to_f16(dv, dv32, nk, g_stream), "k_f2h");
+    if (!st_.err) st_kernel(&st_, aria_k_flash_attn(dq, dk, dv, dout, 0, B * H, H, Nq, Nk, g_stream), "k_flash_attn");
+    st_out(&st_, out, dout, FB(nq));
     HOST_END();
 }
 int aria_hip_linear_q8(float *y, const float *x, const int8_t *q, const float *scale, const float *b, int M,

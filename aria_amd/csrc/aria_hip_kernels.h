@@ -88,6 +88,17 @@ hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtyp
                           const float *scale, const float *bias, int M, int K, int N, int tiles,
                           hipStream_t s);
 
+/* Attention (k_attn.hip). Head preparation: src [B*S, ld] fp32 holds nsec sections of
+ * H*64 columns; kind[i] = 0 (q: RMSNorm w[i] + RoPE), 1 (k: same), 2 (v: copy); each
+ * section is written to dst[i] as fp16 [B, H, S, 64]. rot = 0 skips RoPE. */
+hipError_t aria_k_qkv_prep(const float *src, int ld, int B, int S, int H, int nsec, const int *kind,
+                           uint16_t *const *dst, const float *const *w, const float *cos_t,
+                           const float *sin_t, int rot, float eps, hipStream_t s);
+/* fused attention, head dim 64: q [BH, Nq, 64], k/v [BH, Nk, 64] fp16 -> o [B, Nq, H*64]
+ * (merged heads, fp16 when o_f16 else fp32), scale 1/8 */
+hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, const uint16_t *v, void *o, int o_f16,
+                             int BH, int H, int Nq, int Nk, hipStream_t s);
+
 /* fp32 SIMT GEMM (k_sgemm.hip), batched with element strides sA/sB/sC:
  * C_b[M,N] = alpha * (A_b[M,K] op(B_b)) (+ bias[N]); op(B) = B^T for B_b [N,K]
  * (transB = 1, Linear layout) or B for B_b [K,N] (transB = 0). */

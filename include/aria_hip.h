@@ -145,6 +145,27 @@ int aria_hip_linear_q8_dev(float *dy, const float *dx, const int8_t *dq, const f
 int aria_hip_linear_q4_dev(float *dy, const float *dx, const uint8_t *dq, const float *dscale,
                            const float *db, int M, int K, int N, void *stream);
 
+/* ---- attention (the DiT's, head dim 64) ----
+ * Head preparation, replacing extract_heads + q/k RMSNorm + RoPE of the block
+ * (src/aria_sa3_dit.c:183-194, 222-226): dsrc [B*S, ld] fp32 holds nsec sections of
+ * H*64 columns (e.g. the qkv projection); section i is written to ddst[i] (a host
+ * array of device pointers) as fp16 [B, H, S, 64]. kind[i]: 0 = q, 1 = k (RMSNorm
+ * with dw[i] (may be NULL), eps, then RoPE over rot dims with tables [S, rot/2];
+ * rot 0 = none), 2 = v (copy). kind and ddst/dw are host arrays of nsec entries. */
+int aria_hip_qkv_prep_dev(const float *dsrc, int ld, int B, int S, int H, int nsec, const int *kind,
+                          uint16_t *const *ddst, const float *const *dw, const float *dcos,
+                          const float *dsin, int rot, float eps, void *stream);
+/* Fused attention, replacing aria_attention (src/aria_ops.h:135, src/aria_cpu.c:811-849)
+ * for the DiT: q [B*H, Nq, D], k/v [B*H, Nk, D] fp16 -> dout [B, Nq, H*D] with heads
+ * merged (the layout the output projection reads), fp16 when out_f16 else fp32.
+ * softmax(q k^T / sqrt(D)) v with scores kept on chip. D must be 64. */
+int aria_hip_flash_attention_dev(const uint16_t *dq, const uint16_t *dk, const uint16_t *dv, void *dout,
+                                 int out_f16, int B, int H, int Nq, int Nk, int D, void *stream);
+/* Host form of the fused attention (parity entry): q/k/v fp32 [B*H, N, D] are rounded
+ * to fp16 on the device; out fp32 [B, Nq, H*D]. */
+int aria_hip_attention_f16(float *out, const float *q, const float *k, const float *v, int B, int H,
+                           int Nq, int Nk, int D);
+
 /* Host-pointer forms with the reference's signatures (src/aria_quant.h:43-45, 64-65):
  * allocate, copy in, run, copy out, free; synchronous. Return 0 or an error. */
 int aria_hip_q8_quant(int8_t *q, float *scale, const float *W, int N, int K);
