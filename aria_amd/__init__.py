@@ -97,6 +97,13 @@ SIGNATURES = {
     "aria_hip_qkv_prep_dev": (_i, [_P, _i, _i, _i, _i, _i, _P, _P, _P, _P, _P, _i, _f, _P]),
     "aria_hip_flash_attention_dev": (_i, [_P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _P]),
     "aria_hip_attention_f16": (_i, [_P, _P, _P, _P, _i, _i, _i, _i, _i]),
+    # include/aria_dit.h
+    "aria_hip_dit_block_create": (_P, [_P, _i, _i, _i, _i, _i, _i, _i]),
+    "aria_hip_dit_block_free": (None, [_P]),
+    "aria_hip_dit_block_weight_bytes": (_sz, [_P]),
+    "aria_hip_dit_block_workspace_bytes": (_sz, [_P, _i, _i, _i]),
+    "aria_hip_dit_block_cross_kv_dev": (_i, [_P, _P, _i, _i, _P, _P, _P, _sz, _P]),
+    "aria_hip_dit_block_forward_dev": (_i, [_P, _P, _i, _i, _P, _P, _P, _i, _P, _P, _i, _P, _sz, _P]),
     # include/aria_hip.h: host-pointer forms
     "aria_hip_linear_q8": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
     "aria_hip_linear_q4": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),

@@ -21,6 +21,7 @@
 
 #include "aria_gpu.h"
 #include "aria_hip.h"
+#include "aria_hip_internal.h"
 #include "aria_hip_kernels.h"
 
 #include <math.h>
@@ -104,6 +105,17 @@ static hipStream_t pick(void *stream) { return stream ? (hipStream_t)stream : g_
         hipError_t e_ = (call);                           \
         if (e_ != hipSuccess) return hip_fail(e_, name);  \
     } while (0)
+
+/* shared with the other host files (aria_hip_internal.h) */
+int aria_hip_ensure(void) { return ensure(); }
+int aria_hip_fail(hipError_t e, const char *what) { return hip_fail(e, what); }
+void aria_hip_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof t_err, fmt, ap);
+    va_end(ap);
+}
+hipStream_t aria_hip_stream(void *stream) { return pick(stream); }
 
 int aria_hip_init(void) { return ensure(); }
 const char *aria_hip_last_error(void) { return t_err; }
@@ -447,14 +459,14 @@ int aria_hip_qlinear_ex_dev(void *dy, int y_f16, const void *dx, int x_f16, int 
     if (!x_f16 && K % 32 == 0 && ((uintptr_t)dx & 15u) == 0 &&
         hipMallocAsync(&x16, (size_t)M * K * 2, s) == hipSuccess) {
         hipError_t e = aria_k_f32_to_f16((uint16_t *)x16, (const float *)dx, (size_t)M * K, s);
-        if (e == hipSuccess) e = aria_k_qgemm_t(dy, y_f16, x16, 1, wtype, dq, dscale, db, M, K, N, tiles, s);
+        if (e == hipSuccess) e = aria_k_qgemm_t(dy, y_f16, x16, 1, wtype, dq, dscale, db, M, K, N, tiles, 0, s);
         hipError_t ef = hipFreeAsync(x16, s);
         if (e == hipSuccess) e = ef;
         KCK(e, "k_qgemm (fp16-staged activations)");
         return 0;
     }
     hipGetLastError();   /* a refused pool allocation leaves no sticky error: take the direct path */
-    KCK(aria_k_qgemm_t(dy, y_f16, dx, x_f16, wtype, dq, dscale, db, M, K, N, tiles, s), "k_qgemm");
+    KCK(aria_k_qgemm_t(dy, y_f16, dx, x_f16, wtype, dq, dscale, db, M, K, N, tiles, 0, s), "k_qgemm");
     return 0;
 }
 int aria_hip_qlinear_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,

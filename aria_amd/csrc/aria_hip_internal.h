@@ -1,0 +1,21 @@
+/*
+ * aria_hip_internal.h - internal: runtime helpers shared by the C host files of the
+ * backend (aria_hip.c, aria_hip_dit.c). Hidden from the library's exported ABI.
+ */
+#ifndef ARIA_HIP_INTERNAL_H
+#define ARIA_HIP_INTERNAL_H
+
+#include <hip/hip_runtime_api.h>
+
+#define ARIA_HIDDEN __attribute__((visibility("hidden")))
+
+/* select the library device on this thread; 0 or ARIA_HIP_ENODEV (error text set) */
+ARIA_HIDDEN int aria_hip_ensure(void);
+/* record (and print) a failed HIP call; returns the error code as int */
+ARIA_HIDDEN int aria_hip_fail(hipError_t e, const char *what);
+/* set the per-thread error text */
+ARIA_HIDDEN void aria_hip_set_error(const char *fmt, ...);
+/* the stream to use for a caller's void* (NULL = library stream) */
+ARIA_HIDDEN hipStream_t aria_hip_stream(void *stream);
+
+#endif /* ARIA_HIP_INTERNAL_H */

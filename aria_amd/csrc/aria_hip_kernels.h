@@ -55,6 +55,9 @@ hipError_t aria_k_pingpong(float *x, const float *v, const float *noise, float t
                            size_t n, hipStream_t s);
 /* fp32 -> fp16 (RTNE), n elements. */
 hipError_t aria_k_f32_to_f16(uint16_t *y, const float *x, size_t n, hipStream_t s);
+/* mod[c][b][i] = tssg[c*dim+i] + gcond[b*6*dim + c*dim + i] (gcond may be NULL), c < 6 */
+hipError_t aria_k_mod_chunks(float *mod, const float *tssg, const float *gcond, int B, int dim,
+                             hipStream_t s);
 
 /* Row softmax in place with optional additive mask [rows, cols] (k_softmax.hip). */
 hipError_t aria_k_softmax(float *x, int rows, int cols, const float *mask, hipStream_t s);
@@ -83,10 +86,10 @@ enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2 };
 hipError_t aria_k_qgemm(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                         const float *scale, const float *bias, int M, int K, int N, hipStream_t s);
 /* the same with an explicit workgroup tile: 1 = 128x128, 2 = 128x64, 3 = 64x128,
- * 4 = 64x64 (M x N); 0 = picked from the shape */
+ * 4 = 64x64 (M x N); 0 = picked from the shape; gelu != 0 applies tanh-GELU after bias */
 hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                           const float *scale, const float *bias, int M, int K, int N, int tiles,
-                          hipStream_t s);
+                          int gelu, hipStream_t s);
 
 /* Attention (k_attn.hip). Head preparation: src [B*S, ld] fp32 holds nsec sections of
  * H*64 columns; kind[i] = 0 (q: RMSNorm w[i] + RoPE), 1 (k: same), 2 (v: copy); each

@@ -291,6 +291,27 @@ extern "C" hipError_t aria_k_pingpong(float *x, const float *v, const float *noi
     return hipGetLastError();
 }
 
+/* DiT modulation (src/aria_sa3_dit.c:152-156): mod = to_scale_shift_gate + gcond[b],
+ * written chunk-major mod[c][b][i] (c < 6) so each of the six [B, dim] slices
+ * (scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff) is contiguous. */
+__global__ __launch_bounds__(256) void k_mod_chunks(float *mod, const float *tssg, const float *gcond, int B,
+                                                    int dim, size_t n) {
+    GRID_STRIDE(idx, n) {
+        const int i = (int)(idx % (size_t)dim);
+        const int b = (int)((idx / dim) % (size_t)B);
+        const int c = (int)(idx / ((size_t)dim * B));
+        const float t = tssg[(size_t)c * dim + i];
+        mod[idx] = gcond ? t + gcond[(size_t)b * 6 * dim + (size_t)c * dim + i] : t;
+    }
+}
+extern "C" hipError_t aria_k_mod_chunks(float *mod, const float *tssg, const float *gcond, int B, int dim,
+                                        hipStream_t s) {
+    const size_t n = (size_t)6 * B * dim;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_mod_chunks, stream_grid((n + 3) / 4), dim3(256), 0, s, mod, tssg, gcond, B, dim, n);
+    return hipGetLastError();
+}
+
 /* fp32 -> fp16 RTNE (the reference's k_f32_to_f16 / aria_f32_to_f16_n) */
 __global__ __launch_bounds__(256) void k_f2h4(uint2 *y, const float4 *x, size_t n4) {
     GRID_STRIDE(i, n4) {

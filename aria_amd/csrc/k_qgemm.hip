@@ -50,6 +50,7 @@ struct QArgs {
     int M, K, N;
     int y_f16;
     int nblk;
+    int gelu;   /* epilogue: y = gelu_tanh(acc*scale + b) (the config FFN's activation) */
 };
 
 #define BK 32
@@ -289,6 +290,7 @@ __global__ __launch_bounds__(256) void k_qgemm_mfma(QArgs a, int NT, int T) {
                 float v = acc[i][j][r];
                 if (WT == ARIA_WQ8) v = v * sc;
                 if (a.bias) v = v + bb;
+                if (a.gelu) v = gelu_tanh_f(v);
                 if (a.y_f16) ((uint16_t *)a.y)[(size_t)m * a.N + n] = f2h_bits(v);
                 else ((float *)a.y)[(size_t)m * a.N + n] = v;
             }
@@ -350,6 +352,7 @@ __global__ __launch_bounds__(256) void k_qgemm_simt(QArgs a) {
             float v = acc[i][j];
             if (WT == ARIA_WQ8) v = v * a.scale[n];
             if (a.bias) v = v + a.bias[n];
+            if (a.gelu) v = gelu_tanh_f(v);
             if (a.y_f16) ((uint16_t *)a.y)[(size_t)m * a.N + n] = f2h_bits(v);
             else ((float *)a.y)[(size_t)m * a.N + n] = v;
         }
@@ -404,11 +407,11 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
 
 extern "C" hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                                      const float *scale, const float *bias, int M, int K, int N, int tiles,
-                                     hipStream_t s) {
+                                     int gelu, hipStream_t s) {
     if (M <= 0 || N <= 0) return hipSuccess;
     QArgs a;
     a.y = y; a.x = x; a.q = q; a.scale = scale; a.bias = bias;
-    a.M = M; a.K = K; a.N = N; a.y_f16 = y_f16; a.nblk = (K + 31) / 32;
+    a.M = M; a.K = K; a.N = N; a.y_f16 = y_f16; a.nblk = (K + 31) / 32; a.gelu = gelu;
     if (wtype == ARIA_WQ8) return x_f16 ? launch_q<ARIA_WQ8, true>(a, tiles, s) : launch_q<ARIA_WQ8, false>(a, tiles, s);
     if (wtype == ARIA_WQ4) return x_f16 ? launch_q<ARIA_WQ4, true>(a, tiles, s) : launch_q<ARIA_WQ4, false>(a, tiles, s);
     if (wtype == ARIA_WF16)
@@ -418,5 +421,5 @@ extern "C" hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f1
 
 extern "C" hipError_t aria_k_qgemm(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                                    const float *scale, const float *bias, int M, int K, int N, hipStream_t s) {
-    return aria_k_qgemm_t(y, y_f16, x, x_f16, wtype, q, scale, bias, M, K, N, 0, s);
+    return aria_k_qgemm_t(y, y_f16, x, x_f16, wtype, q, scale, bias, M, K, N, 0, 0, s);
 }

@@ -264,6 +264,9 @@ def main():
 
     # C3: Q8 / Q4 dequant-on-use GEMMs at M = 2592 (fp32 activations, as aria_linear_q8/q4 take)
     gemm = gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps)
+    del sets
+    # C4: one q4 DiT block at T = 1296, batch 2
+    block = block_leg(DeviceArray, time_loop, stream, rng, reps)
 
     dom = max(OPS, key=lambda o: ops_report[o]["us"])
     dom_us = ops_report[dom]["us"]
@@ -294,7 +297,8 @@ def main():
         "cpu_baseline": cpu,
         "ops": ops_report,
         "gemm": gemm,
-        "block_us": None,
+        "block_us": block["gelu"]["us"],
+        "block": block,
         "wall_s_timed": round(t_wall, 3),
     }
     print(json.dumps(line), flush=True)
@@ -325,6 +329,41 @@ def gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps):
             key = f"{'q8' if wt == 0 else 'q4'}_M{M}_K{K}_N{N}"
             out[key] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
                         "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 3), "flop": flop}
+    return out
+
+
+def block_leg(DeviceArray, time_loop, stream, rng, reps):
+    """Config 4: one random-init q4 DiT block (attention projections Q8, FFN Q4, ca_to_kv fp16),
+    x [2,1296,1024] ~N(0,1), cond [2,256,768] ~N(0,1), weights ~N(0,0.02), gains 1+N(0,0.02),
+    modulation [2, 6*1024] ~N(0,0.1), 16 heads x 64, RoPE rot 32. Timed: the block forward
+    (the per-request cross K/V projection runs once, outside)."""
+    from aria_amd.dit import DitBlock, random_block_weights, FFN_GELU, FFN_GLU, Q4
+    Bb, Sb, Sc, dim, H, inner, dctx = B, S, 256, 1024, 16, 4096, 768
+    M = Bb * Sb
+    out = {}
+    inv = 1.0 / (10000.0 ** (np.arange(16) * 2.0 / 32))
+    ang = np.arange(Sb)[:, None] * inv[None, :]
+    dcos = DeviceArray.from_host(np.cos(ang).astype(np.float32))
+    dsin = DeviceArray.from_host(np.sin(ang).astype(np.float32))
+    for name, ffn in (("gelu", FFN_GELU), ("glu", FFN_GLU)):
+        W = random_block_weights(rng, dim, inner, dctx, ffn=ffn)
+        blk = DitBlock(W, dim, H, inner, dctx, ffn=ffn, precision=Q4)
+        dctxa = DeviceArray.from_host(rng.standard_normal((Bb * Sc, dctx), dtype=np.float32))
+        dk, dv = blk.cross_kv(dctxa, Bb, Sc, stream)
+        dx = DeviceArray.from_host(rng.standard_normal((M, dim), dtype=np.float32))
+        dg = DeviceArray.from_host((0.1 * rng.standard_normal((Bb, 6 * dim))).astype(np.float32))
+        ws = blk.workspace(Bb, Sb, Sc)
+
+        def fwd(i):
+            blk.forward(dx, Bb, Sb, dg, dk, dv, Sc, dcos, dsin, 32, ws=ws, stream=stream)
+            return 0
+        ms = time_loop(fwd, reps)
+        ffrows = 2 * inner if ffn == FFN_GLU else inner
+        flop = 2.0 * M * dim * (3 * dim + dim + dim + dim) + 2.0 * M * dim * (ffrows + inner) \
+            + 2 * 2.0 * Bb * H * Sb * Sb * 64 + 2 * 2.0 * Bb * H * Sb * Sc * 64
+        out[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "flop": flop,
+                     "weight_bytes": blk.weight_bytes}
+        blk.free()
     return out
 
 

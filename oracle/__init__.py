@@ -182,6 +182,39 @@ class _Lib:
         # the reference's elementwise ops take int n; the port takes size_t
         return _sz(n) if self.p == "or_" else _i(n)
 
+    def dit_block_forward(self, x, ctx, gcond, cos_t, sin_t, rot, W, num_heads, inner):
+        """The reference's own fp32 block forward, aria_dit_block_forward
+        (src/aria_sa3_dit.c:316-349 -> dit_block_core :141-312), batch 1, SiLU-GLU FFN.
+        x [S, dim] (not modified; returns the new residual stream), ctx [Sc, dim_ctx],
+        gcond [6*dim], W: dict of the aria_dit_block_w fields (fp32)."""
+        if self.p != "aria_":
+            raise RuntimeError("dit_block_forward exists only in the compiled reference")
+        S, dim = x.shape
+        Sc, dim_ctx = ctx.shape
+        keep = {k: np.ascontiguousarray(v, np.float32) for k, v in W.items() if v is not None}
+        w = BlockW()
+        for f in BLOCK_FIELDS:
+            a = keep.get(f)
+            setattr(w, f, a.ctypes.data if a is not None else None)
+        y = np.ascontiguousarray(x, np.float32).copy()
+        ctx = np.ascontiguousarray(ctx, np.float32)
+        gcond = np.ascontiguousarray(gcond, np.float32)
+        self.lib.aria_dit_block_forward(_fp(y), _i(S), _i(dim), _i(num_heads), _i(dim // num_heads), _i(inner),
+                                        _fp(ctx), _i(Sc), _i(dim_ctx), _fp(gcond), _fp(cos_t), _fp(sin_t),
+                                        _i(rot), C.byref(w), _i(0))
+        return y
+
+
+# aria_dit_block_w, src/aria_sa3_dit.h:40-48 (21 pointers in this order)
+BLOCK_FIELDS = ("pre_norm", "cross_norm", "ff_norm", "sa_to_qkv", "sa_q_norm", "sa_k_norm", "sa_to_out",
+                "ca_to_q", "ca_to_kv", "ca_q_norm", "ca_k_norm", "ca_to_out", "ff_in_w", "ff_in_b",
+                "ff_out_w", "ff_out_b", "to_scale_shift_gate", "to_local0_w", "to_local0_b", "to_local2_w",
+                "to_local2_b")
+
+
+class BlockW(C.Structure):
+    _fields_ = [(f, C.c_void_p) for f in BLOCK_FIELDS]
+
 
 class Port(_Lib):
     """The restatement: extra functions that the reference has only as static glue."""

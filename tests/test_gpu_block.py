@@ -1,0 +1,89 @@
+"""GPU parity of one DiT block (config 4) through the C ABI (include/aria_dit.h).
+
+Oracles, per sequence of the batch:
+  * SA3 SiLU-GLU block: the reference's own aria_dit_block_forward (compiled from its
+    src/aria_sa3_dit.c) run on the dequantized weights, which is what dequant-on-use computes;
+  * config-literal tanh-GELU block: the composition of reference ops in dit_block_core's
+    order (oracle/dit_block.py, pinned against aria_dit_block_forward in test_oracle.py).
+Gate: the reference's block parity gate, max|d| <= 1e-3 + 3e-3 * max|ref| (tests/test_dit.c:86);
+the packed weights are also checked bit-exact against the reference quantizer.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, randn, rng
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-3, 3e-3
+
+
+def run_block(W, x, ctx, gcond, H, inner, dim_ctx, ffn, precision, rot, cos_t, sin_t):
+    from aria_amd.device import DeviceArray, sync
+    from aria_amd.dit import DitBlock
+    B, S, dim = x.shape
+    Sc = ctx.shape[1]
+    blk = DitBlock(W, dim, H, inner, dim_ctx, ffn=ffn, precision=precision)
+    dctx = DeviceArray.from_host(ctx.reshape(B * Sc, dim_ctx))
+    dk, dv = blk.cross_kv(dctx, B, Sc)
+    dx = DeviceArray.from_host(x.reshape(B * S, dim))
+    dg = DeviceArray.from_host(gcond)
+    dc, ds = DeviceArray.from_host(cos_t), DeviceArray.from_host(sin_t)
+    blk.forward(dx, B, S, dg, dk, dv, Sc, dc, ds, rot)
+    sync()
+    return dx.to_host().reshape(B, S, dim)
+
+
+def case(seed, B, S, Sc, dim, inner, dim_ctx, ffn):
+    from aria_amd.dit import random_block_weights
+    r = rng(seed)
+    W = random_block_weights(r, dim, inner, dim_ctx, ffn=ffn)
+    x = randn(r, (B, S, dim)); ctx = randn(r, (B, Sc, dim_ctx)); gcond = randn(r, (B, 6 * dim), 0.1)
+    return W, x, ctx, gcond
+
+
+def reference_blocks(ref, port, W, x, ctx, gcond, H, inner, precision, rot, c, s, ffn):
+    from oracle import dit_block as DB
+    packed = DB.pack_weights(ref, W, precision)
+    out = []
+    for b in range(x.shape[0]):
+        if ffn == DB.FFN_GLU:
+            Wd = DB.dequantized(port, W, packed)
+            out.append(ref.dit_block_forward(x[b], ctx[b], gcond[b], c, s, rot, Wd, H, inner))
+        else:
+            kc, vc = DB.cross_kv(ref, ctx[b], W, H)
+            out.append(DB.block_forward(ref, port, x[b], kc, vc, gcond[b], W, packed, c, s, rot, H, ffn))
+    return np.stack(out)
+
+
+@pytest.fixture
+def R(ref):
+    if ref is None:
+        pytest.skip("oracle/_ref not built: the block oracle needs the compiled reference")
+    return ref
+
+
+@pytest.mark.parametrize("precision", [4, 3, 0])      # ARIA_Q4, ARIA_Q8, ARIA_F32 (fp16 weights)
+def test_block_small(hip, port, R, precision):
+    B, S, Sc, dim, H, inner, dim_ctx = 2, 70, 24, 256, 4, 512, 64
+    W, x, ctx, gcond = case(7 + precision, B, S, Sc, dim, inner, dim_ctx, 0)
+    c, s = R.rope_freqs(S, 32, 10000.0)
+    got = run_block(W, x, ctx, gcond, H, inner, dim_ctx, 0, precision, 32, c, s)
+    pname = {4: "q4", 3: "q8", 0: "f32"}[precision]
+    want = reference_blocks(R, port, W, x, ctx, gcond, H, inner, pname, 32, c, s, 0)
+    assert_close(got, want, ATOL, RTOL, f"block {pname}")
+
+
+@pytest.mark.parametrize("ffn", [1, 0])               # config-literal GELU, SA3 GLU
+def test_block_config4_full(hip, port, R, ffn):
+    """Config 4: x [2,1296,1024], cond [2,256,768], 16 heads x 64, q4 recipe, RoPE rot 32."""
+    B, S, Sc, dim, H, inner, dim_ctx = 2, 1296, 256, 1024, 16, 4096, 768
+    W, x, ctx, gcond = case(0xA21A0004 + ffn, B, S, Sc, dim, inner, dim_ctx, ffn)
+    c, s = R.rope_freqs(S, 32, 10000.0)
+    got = run_block(W, x, ctx, gcond, H, inner, dim_ctx, ffn, 4, 32, c, s)
+    want = reference_blocks(R, port, W, x, ctx, gcond, H, inner, "q4", 32, c, s, ffn)
+    d = np.abs(got - want)
+    print(f"ffn={ffn}: max|d| {d.max():.3e}  rms {np.sqrt((d ** 2).mean()):.3e}  max|ref| {np.abs(want).max():.2f}")
+    assert_close(got, want, ATOL, RTOL, f"config-4 block ffn={ffn}")

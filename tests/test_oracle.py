@@ -284,3 +284,38 @@ def test_fused_chain_is_composition(port):
     m = n * (1 + sc[:, None, :]) + sh[:, None, :]
     gl = 0.5 * m * (1 + np.tanh(0.7978845608028654 * (m + 0.044715 * m ** 3)))
     assert np.max(np.abs(out - (gl + x64))) < 2e-5
+
+
+def _block_case(seed, dim=128, H=2, S=40, Sc=12, inner=256, dim_ctx=64):
+    from oracle.dit_block import FFN_GLU  # noqa: F401
+    r = rng(seed)
+
+    def n(shape, s=0.02):
+        return (s * r.standard_normal(shape)).astype(np.float32)
+    W = {"pre_norm": 1 + n(dim), "cross_norm": 1 + n(dim), "ff_norm": 1 + n(dim),
+         "sa_to_qkv": n((3 * dim, dim), 0.1), "sa_q_norm": 1 + n(64), "sa_k_norm": 1 + n(64),
+         "sa_to_out": n((dim, dim), 0.1), "ca_to_q": n((dim, dim), 0.1), "ca_to_kv": n((2 * dim, dim_ctx), 0.1),
+         "ca_q_norm": 1 + n(64), "ca_k_norm": 1 + n(64), "ca_to_out": n((dim, dim), 0.1),
+         "ff_in_w": n((2 * inner, dim), 0.1), "ff_in_b": n(2 * inner), "ff_out_w": n((dim, inner), 0.1),
+         "ff_out_b": n(dim), "to_scale_shift_gate": n(6 * dim, 0.1)}
+    x = randn(r, (S, dim)); ctx = randn(r, (Sc, dim_ctx)); gcond = randn(r, 6 * dim, 0.1)
+    return W, x, ctx, gcond, dim, H, S, Sc, inner
+
+
+@pytest.mark.parametrize("precision", ["f32", "q8", "q4"])
+def test_block_composition_matches_reference_block(port, R, precision):
+    """oracle/dit_block.py (reference ops composed in dit_block_core's order) against the
+    reference's own aria_dit_block_forward (src/aria_sa3_dit.c:316-349) run on the
+    dequantized weights: the same block, so the results agree to summation order."""
+    from oracle import dit_block as DB
+    W, x, ctx, gcond, dim, H, S, Sc, inner = _block_case(21)
+    c, s = R.rope_freqs(S, 32, 10000.0)
+    packed = DB.pack_weights(R, W, precision)
+    Wd = DB.dequantized(port, W, packed)
+    want = R.dit_block_forward(x, ctx, gcond, c, s, 32, Wd, H, inner)
+    kc, vc = DB.cross_kv(R, ctx, W, H)
+    got = DB.block_forward(R, port, x, kc, vc, gcond, W, packed, c, s, 32, H, DB.FFN_GLU)
+    assert_close(got, want, 1e-5, 1e-5, f"block {precision}")
+    # a plausible composition mistake (RoPE left out of the self-attention) is caught
+    wrong = DB.block_forward(R, port, x, kc, vc, gcond, W, packed, c, s, 0, H, DB.FFN_GLU)
+    assert not np.allclose(wrong, want, atol=1e-4)
