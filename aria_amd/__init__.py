@@ -104,6 +104,24 @@ SIGNATURES = {
     "aria_hip_dit_block_workspace_bytes": (_sz, [_P, _i, _i, _i]),
     "aria_hip_dit_block_cross_kv_dev": (_i, [_P, _P, _i, _i, _P, _P, _P, _sz, _P]),
     "aria_hip_dit_block_forward_dev": (_i, [_P, _P, _i, _i, _P, _P, _P, _i, _P, _P, _i, _P, _sz, _P]),
+    "aria_cuda_dit_create": (_P, [_P, _i]),
+    "aria_cuda_dit_free": (None, [_P]),
+    "aria_cuda_dit_set_request": (None, [_P, _P]),
+    "aria_cuda_dit_set_step": (None, [_P, _i]),
+    "aria_cuda_dit_step": (None, [_P, _P, _P, _P]),
+    "aria_cuda_dit_sample": (_i, [_P, _P, _P, _i, _P, _P, _P, _P, _P]),
+    "aria_hip_dit_create_ex": (_P, [_P, _i, _i]),
+    "aria_hip_dit_set_request_batch": (_i, [_P, _P, _i]),
+    "aria_hip_dit_step_batch": (_i, [_P, _P, _P, _P]),
+    "aria_hip_dit_device_buffers": (_i, [_P, _P, _P, _P]),
+    "aria_hip_dit_run": (_i, [_P, _P]),
+    "aria_hip_dit_graph_active": (_i, [_P]),
+    "aria_cuda_dec_create": (_P, [_P]),
+    "aria_cuda_dec_free": (None, [_P]),
+    "aria_cuda_dec_forward": (None, [_P, _P, _P, _i]),
+    "aria_cuda_dec_medium_create": (_P, [_P]),
+    "aria_cuda_dec_medium_free": (None, [_P]),
+    "aria_cuda_dec_medium_forward": (None, [_P, _P, _P, _i]),
     # include/aria_hip.h: host-pointer forms
     "aria_hip_linear_q8": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
     "aria_hip_linear_q4": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),

@@ -29,6 +29,7 @@
 #include "aria_hip_internal.h"
 #include "aria_hip_kernels.h"
 
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -237,11 +238,24 @@ int aria_hip_dit_block_cross_kv_dev(aria_hip_dit_block *b, const float *dctx, in
     return 0;
 }
 
+static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const float *dgcond, const uint16_t *dk,
+                         const uint16_t *dv, int Sc, const float *dcos, const float *dsin, int rot,
+                         const float *dlocal, void *dws, size_t ws_bytes, hipStream_t s);
+
 int aria_hip_dit_block_forward_dev(aria_hip_dit_block *b, float *dx, int B, int S, const float *dgcond,
                                    const uint16_t *dk, const uint16_t *dv, int Sc, const float *dcos,
                                    const float *dsin, int rot, void *dws, size_t ws_bytes, void *stream) {
     int rc = aria_hip_ensure();
     if (rc) return rc;
+    return block_forward(b, dx, B, S, dgcond, dk, dv, Sc, dcos, dsin, rot, NULL, dws, ws_bytes,
+                         aria_hip_stream(stream));
+}
+
+/* dlocal: the inpaint local-additive conditioning [B*S, dim] added after the cross-attention
+ * (src/aria_sa3_dit.c:248-252), or NULL */
+static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const float *dgcond, const uint16_t *dk,
+                         const uint16_t *dv, int Sc, const float *dcos, const float *dsin, int rot,
+                         const float *dlocal, void *dws, size_t ws_bytes, hipStream_t s) {
     if (!b || B <= 0 || S <= 0 || Sc <= 0 || !dx || !dk || !dv || !dws || (rot && (!dcos || !dsin)) ||
         (rot != 0 && rot != 32 && rot != 64)) {
         aria_hip_set_error("aria_hip_dit_block_forward_dev: invalid argument");
@@ -252,7 +266,6 @@ int aria_hip_dit_block_forward_dev(aria_hip_dit_block *b, float *dx, int B, int 
         aria_hip_set_error("aria_hip_dit_block_forward_dev: workspace too small");
         return ARIA_HIP_EINVAL;
     }
-    hipStream_t s = aria_hip_stream(stream);
     const int d = b->dim, H = b->H, M = B * S;
     const size_t Bd = (size_t)B * d;
     const float eps_norm = 1e-5f, eps_qk = 1e-6f;
@@ -288,6 +301,7 @@ int aria_hip_dit_block_forward_dev(aria_hip_dit_block *b, float *dx, int B, int 
     STEP(aria_k_flash_attn(w.q16, dk, dv, w.att16, 1, B * H, H, S, Sc, s), "k_flash_attn (cross)");
     STEP(gemm(&b->ca_out, w.o, 0, w.att16, NULL, M, 0, s), "k_qgemm (ca_to_out)");
     STEP(aria_k_add(dx, dx, w.o, (size_t)M * d, s), "k_add (cross residual)");
+    if (dlocal) STEP(aria_k_add(dx, dx, dlocal, (size_t)M * d, s), "k_add (local cond)");
 
     /* ---- feed-forward ---- */
     STEP(aria_k_rownorm(w.h16, 1, dx, b->ff_norm, NULL, scale_ff, shift_ff, S, 0, 0, ARIA_NORM_RMS, M, d, eps_norm, s),
@@ -301,4 +315,424 @@ int aria_hip_dit_block_forward_dev(aria_hip_dit_block *b, float *dx, int B, int 
     STEP(gemm(&b->ff_out, w.o, 0, w.ff16, NULL, M, 0, s), "k_qgemm (ff_out)");
     STEP(aria_k_gate_residual(dx, dx, w.o, gate_ff, b->ff_out_b, M, d, S, s), "k_gate_residual (ff)");
     return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* device-resident DiT (the reference's aria_cuda_dit_* ABI)                 */
+/* ------------------------------------------------------------------------- */
+
+struct aria_cuda_dit {
+    int depth, ed, H, inner, io_ch, n_mem, rot;
+    aria_hip_dit_block **blk;
+    float *pre, *post, *pin, *pout, *mem;   /* fp32: [C,C], [C,C], [ed,C], [C,ed], [n_mem, ed] */
+    hipStream_t st;
+    /* request state */
+    int have_req, B, T, S, Sc, cur_step;
+    uint16_t **ck, **cv;                    /* [depth] each [B, H, Sc, 64] */
+    float *cos_t, *sin_t;                   /* [S, rot/2] */
+    float **local;                          /* [depth] each [B*S, ed], or NULL */
+    const aria_steer_set *steer;
+    float *saved_ced;                       /* host copy of the B context embeddings */
+    void *ws;
+    size_t ws_bytes;
+    float *dx, *dv, *dgcond, *dxtc, *dtmp, *dseq, *dout, *dnoise;
+    /* captured step */
+    hipGraph_t graph;
+    hipGraphExec_t gexec;
+    int graph_ready, graph_failed, no_graph;
+    /* pinned staging for the sampler */
+    float *pin_gc, *pin_nz[2];
+    size_t pin_gc_n, pin_nz_n;
+};
+
+static int up_mat(float **d, const float *h, size_t n) {
+    *d = NULL;
+    if (!h) return 0;
+    return upv(d, h, n, NULL);
+}
+
+static void req_free(aria_cuda_dit *h) {
+    if (h->gexec) hipGraphExecDestroy(h->gexec);
+    if (h->graph) hipGraphDestroy(h->graph);
+    h->gexec = NULL; h->graph = NULL; h->graph_ready = 0; h->graph_failed = 0;
+    if (h->ck) for (int b = 0; b < h->depth; b++) { dfree(h->ck[b]); dfree(h->cv[b]); }
+    if (h->local) for (int b = 0; b < h->depth; b++) dfree(h->local[b]);
+    free(h->ck); free(h->cv); free(h->local);
+    h->ck = h->cv = NULL; h->local = NULL;
+    float *bufs[] = {h->cos_t, h->sin_t, h->dx, h->dv, h->dgcond, h->dxtc, h->dtmp, h->dseq, h->dout, h->dnoise};
+    for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) dfree(bufs[i]);
+    h->cos_t = h->sin_t = h->dx = h->dv = h->dgcond = h->dxtc = h->dtmp = h->dseq = h->dout = h->dnoise = NULL;
+    dfree(h->ws);
+    h->ws = NULL; h->ws_bytes = 0;
+    free(h->saved_ced);
+    h->saved_ced = NULL;
+    h->have_req = 0;
+}
+
+void aria_cuda_dit_free(aria_cuda_dit *h) {
+    if (!h) return;
+    if (aria_hip_ensure() == 0) hipStreamSynchronize(h->st);
+    req_free(h);
+    if (h->blk) for (int b = 0; b < h->depth; b++) aria_hip_dit_block_free(h->blk[b]);
+    free(h->blk);
+    float *w[] = {h->pre, h->post, h->pin, h->pout, h->mem};
+    for (size_t i = 0; i < sizeof w / sizeof *w; i++) dfree(w[i]);
+    if (h->pin_gc) hipHostFree(h->pin_gc);
+    if (h->pin_nz[0]) hipHostFree(h->pin_nz[0]);
+    if (h->pin_nz[1]) hipHostFree(h->pin_nz[1]);
+    if (h->st) hipStreamDestroy(h->st);
+    free(h);
+}
+
+aria_cuda_dit *aria_hip_dit_create_ex(const aria_sa3_dit_view *v, aria_dtype precision, int ffn) {
+    if (aria_hip_ensure() || !v || !v->blocks) return NULL;
+    if (v->differential || v->head_dim != 64 || v->num_heads * v->head_dim != v->ed || v->depth <= 0 ||
+        v->io_ch <= 0 || v->n_mem < 0 || (v->rot_dim != 0 && v->rot_dim != 32 && v->rot_dim != 64)) {
+        aria_hip_set_error("aria_cuda_dit_create: unsupported model shape");
+        return NULL;
+    }
+    if (precision == ARIA_DTYPE_AUTO) precision = ARIA_F32;   /* aria_cuda_int8_tc() == 0 here */
+    aria_cuda_dit *h = (aria_cuda_dit *)calloc(1, sizeof *h);
+    if (!h) return NULL;
+    h->depth = v->depth; h->ed = v->ed; h->H = v->num_heads; h->inner = v->inner; h->io_ch = v->io_ch;
+    h->n_mem = v->n_mem; h->rot = v->rot_dim;
+    const char *ng = getenv("ARIA_NO_GRAPH");   /* read once per handle */
+    h->no_graph = ng && ng[0] && ng[0] != '0';
+    if (hipStreamCreateWithFlags(&h->st, hipStreamNonBlocking) != hipSuccess) { free(h); return NULL; }
+    /* VRAM fit: packed blocks (<= fp16 size) + fp32 io projections, with margin */
+    size_t fr = 0, tot = 0;
+    hipMemGetInfo(&fr, &tot);
+    const size_t per_block = ((size_t)10 * v->ed * v->ed + (size_t)(ffn == ARIA_FFN_GLU ? 3 : 2) * v->inner * v->ed) * 2;
+    if ((size_t)v->depth * per_block + ((size_t)256 << 20) > fr) {
+        aria_hip_set_error("aria_cuda_dit_create: model does not fit in device memory");
+        aria_cuda_dit_free(h);
+        return NULL;
+    }
+    h->blk = (aria_hip_dit_block **)calloc((size_t)v->depth, sizeof *h->blk);
+    int rc = h->blk ? 0 : ARIA_HIP_ENOMEM;
+    for (int b = 0; b < v->depth && !rc; b++) {
+        h->blk[b] = aria_hip_dit_block_create(&v->blocks[b], v->ed, v->num_heads, 64, v->inner, ffn, v->ed,
+                                              precision);
+        if (!h->blk[b]) rc = ARIA_HIP_EINVAL;
+    }
+    const size_t C = (size_t)v->io_ch, E = (size_t)v->ed;
+    if (!rc) rc = up_mat(&h->pre, v->preprocess, C * C);
+    if (!rc) rc = up_mat(&h->post, v->postprocess, C * C);
+    if (!rc) rc = up_mat(&h->pin, v->project_in, E * C);
+    if (!rc) rc = up_mat(&h->pout, v->project_out, C * E);
+    if (!rc && v->n_mem) rc = up_mat(&h->mem, v->memory_tokens, (size_t)v->n_mem * E);
+    if (!rc && (!h->pin || !h->pout)) rc = ARIA_HIP_EINVAL;
+    if (rc) {
+        aria_cuda_dit_free(h);
+        return NULL;
+    }
+    return h;
+}
+
+aria_cuda_dit *aria_cuda_dit_create(const aria_sa3_dit_view *v, aria_dtype precision) {
+    return aria_hip_dit_create_ex(v, precision, ARIA_FFN_GLU);
+}
+
+/* warm hit (src/aria_cuda.cu:1268-1285): the same shapes and context embeddings as the
+ * current request, no local cond and no steering -> keep the graph and K/V caches */
+static int req_same(const aria_cuda_dit *h, const aria_sa3_dit_req_view *rv, int B) {
+    if (!h->have_req || !h->saved_ced || h->B != B || h->local) return 0;
+    for (int i = 0; i < B; i++) {
+        if (!rv[i].cross_ed || rv[i].has_local || (rv[i].steer && rv[i].steer->n > 0)) return 0;
+        if (rv[i].S != h->S || rv[i].T != h->T || rv[i].n_cond != h->Sc) return 0;
+        if (memcmp(h->saved_ced + (size_t)i * h->Sc * h->ed, rv[i].cross_ed, (size_t)h->Sc * h->ed * sizeof(float)))
+            return 0;
+    }
+    return 1;
+}
+
+static int req_setup(aria_cuda_dit *h, const aria_sa3_dit_req_view *rv, int B) {
+    int rc = aria_hip_ensure();
+    if (rc) return rc;
+    if (!h || !rv || B <= 0) return ARIA_HIP_EINVAL;
+    if (req_same(h, rv, B)) {
+        h->cur_step = 0;
+        h->steer = NULL;
+        return 0;
+    }
+    const int T = rv[0].T, S = rv[0].S, Sc = rv[0].n_cond;
+    for (int i = 0; i < B; i++)
+        if (rv[i].T != T || rv[i].S != S || rv[i].n_cond != Sc || S != h->n_mem + T || T <= 0 || Sc <= 0 ||
+            (!rv[i].cross_ed && (!rv[i].cross_k || !rv[i].cross_v)) || (h->rot && (!rv[i].rope_cos || !rv[i].rope_sin))) {
+            aria_hip_set_error("aria_hip_dit_set_request: request views disagree or lack context K/V");
+            return ARIA_HIP_EINVAL;
+        }
+    hipStreamSynchronize(h->st);
+    req_free(h);
+    h->B = B; h->T = T; h->S = S; h->Sc = Sc; h->steer = rv[0].steer; h->cur_step = 0;
+    const int E = h->ed, C = h->io_ch, H = h->H, rh = h->rot / 2;
+    size_t need = aria_hip_dit_block_workspace_bytes(h->blk[0], B, S, Sc);
+    rc = dalloc(&h->ws, need, NULL);
+    h->ws_bytes = need;
+    const size_t nxc = (size_t)B * C * T;
+    float **step_bufs[] = {&h->dx, &h->dv, &h->dxtc, &h->dtmp, &h->dout, &h->dnoise};
+    for (size_t i = 0; i < sizeof step_bufs / sizeof *step_bufs && !rc; i++)
+        rc = dalloc((void **)step_bufs[i], nxc * 4, NULL);
+    if (!rc) rc = dalloc((void **)&h->dgcond, (size_t)B * 6 * E * 4, NULL);
+    if (!rc) rc = dalloc((void **)&h->dseq, (size_t)B * S * E * 4, NULL);
+    if (!rc && rh) {
+        rc = upv(&h->cos_t, rv[0].rope_cos, (size_t)S * rh, NULL);
+        if (!rc) rc = upv(&h->sin_t, rv[0].rope_sin, (size_t)S * rh, NULL);
+    }
+    h->ck = (uint16_t **)calloc((size_t)h->depth, sizeof *h->ck);
+    h->cv = (uint16_t **)calloc((size_t)h->depth, sizeof *h->cv);
+    if (!rc && (!h->ck || !h->cv)) rc = ARIA_HIP_ENOMEM;
+    const size_t khv = (size_t)H * Sc * 64;   /* one sequence's K (or V) of one block */
+    for (int b = 0; b < h->depth && !rc; b++) {
+        rc = dalloc((void **)&h->ck[b], B * khv * 2, NULL);
+        if (!rc) rc = dalloc((void **)&h->cv[b], B * khv * 2, NULL);
+    }
+    float *tmp = NULL;
+    if (!rc && rv[0].cross_ed) {
+        /* cross K/V of every block projected on the device from the B context embeddings
+         * stacked [B*Sc, ed] (src/aria_cuda.cu:1324-1353) */
+        rc = dalloc((void **)&tmp, (size_t)B * Sc * E * 4, NULL);
+        for (int i = 0; i < B && !rc; i++) {
+            hipError_t e = hipMemcpy(tmp + (size_t)i * Sc * E, rv[i].cross_ed, (size_t)Sc * E * 4, hipMemcpyHostToDevice);
+            if (e != hipSuccess) rc = FAIL(e, "hipMemcpy (cross_ed)");
+        }
+        for (int b = 0; b < h->depth && !rc; b++)
+            rc = aria_hip_dit_block_cross_kv_dev(h->blk[b], tmp, B, Sc, h->ck[b], h->cv[b], h->ws, h->ws_bytes, h->st);
+        if (!rc) {
+            h->saved_ced = (float *)malloc((size_t)B * Sc * E * sizeof(float));
+            for (int i = 0; i < B && h->saved_ced; i++)
+                memcpy(h->saved_ced + (size_t)i * Sc * E, rv[i].cross_ed, (size_t)Sc * E * sizeof(float));
+        }
+    } else if (!rc) {
+        /* legacy: host-projected fp32 K/V [H, Sc, 64] per block, converted to fp16 here */
+        rc = dalloc((void **)&tmp, B * khv * 2 * 4, NULL);
+        for (int b = 0; b < h->depth && !rc; b++) {
+            for (int i = 0; i < B && !rc; i++) {
+                hipError_t e = hipMemcpy(tmp + i * khv, rv[i].cross_k[b], khv * 4, hipMemcpyHostToDevice);
+                if (e == hipSuccess)
+                    e = hipMemcpy(tmp + (B + i) * khv, rv[i].cross_v[b], khv * 4, hipMemcpyHostToDevice);
+                if (e != hipSuccess) rc = FAIL(e, "hipMemcpy (cross K/V)");
+            }
+            if (!rc) {
+                hipError_t e = aria_k_f32_to_f16(h->ck[b], tmp, B * khv, h->st);
+                if (e == hipSuccess) e = aria_k_f32_to_f16(h->cv[b], tmp + B * khv, B * khv, h->st);
+                if (e == hipSuccess) e = hipStreamSynchronize(h->st);
+                if (e != hipSuccess) rc = FAIL(e, "cross K/V upload");
+            }
+        }
+    }
+    /* inpaint local-additive cond per block, [S, ed] per sequence (zeros where absent) */
+    int any_local = 0;
+    for (int i = 0; i < B; i++) any_local |= rv[i].has_local && rv[i].local_emb;
+    if (!rc && any_local) {
+        h->local = (float **)calloc((size_t)h->depth, sizeof *h->local);
+        if (!h->local) rc = ARIA_HIP_ENOMEM;
+        for (int b = 0; b < h->depth && !rc; b++) {
+            rc = dalloc((void **)&h->local[b], (size_t)B * S * E * 4, NULL);
+            for (int i = 0; i < B && !rc; i++) {
+                const float *src = rv[i].has_local && rv[i].local_emb ? rv[i].local_emb[b] : NULL;
+                hipError_t e = src ? hipMemcpy(h->local[b] + (size_t)i * S * E, src, (size_t)S * E * 4,
+                                               hipMemcpyHostToDevice)
+                                   : hipMemset(h->local[b] + (size_t)i * S * E, 0, (size_t)S * E * 4);
+                if (e != hipSuccess) rc = FAIL(e, "local cond upload");
+            }
+        }
+    }
+    if (!rc) {
+        hipError_t e = hipStreamSynchronize(h->st);
+        if (e != hipSuccess) rc = FAIL(e, "set_request");
+    }
+    dfree(tmp);
+    if (!rc && h->steer && h->steer->n > 0) {
+        static int warned;
+        if (!warned++) fprintf(stderr, "[aria-hip] residual steering is not applied by this backend\n");
+    }
+    if (rc) { req_free(h); return rc; }
+    h->have_req = 1;
+    return 0;
+}
+
+void aria_cuda_dit_set_request(aria_cuda_dit *h, const aria_sa3_dit_req_view *rv) { req_setup(h, rv, 1); }
+int aria_hip_dit_set_request_batch(aria_cuda_dit *h, const aria_sa3_dit_req_view *rv, int B) {
+    return req_setup(h, rv, B);
+}
+void aria_cuda_dit_set_step(aria_cuda_dit *h, int step) {
+    if (h) h->cur_step = step;
+}
+
+/* one velocity evaluation on the handle's buffers (src/aria_sa3_dit.c:734-777):
+ * [C,T] -> [T,C]; xtc += preprocess(xtc); seq = [memory tokens | project_in(xtc)];
+ * depth blocks; out = project_out(seq[n_mem:]); out += postprocess(out); -> [C,T] */
+static int step_compute(aria_cuda_dit *h, hipStream_t s) {
+    const int B = h->B, T = h->T, S = h->S, C = h->io_ch, E = h->ed, Mt = h->n_mem;
+    const size_t nxc = (size_t)B * T * C;
+    STEP(aria_k_transpose(h->dxtc, h->dx, C, T, B, s), "k_transpose (x)");
+    if (h->pre) {
+        STEP(aria_k_sgemm(h->dtmp, h->dxtc, h->pre, NULL, B * T, C, C, 1, 1.0f, 1, 0, 0, 0, s), "preprocess");
+        STEP(aria_k_add(h->dxtc, h->dxtc, h->dtmp, nxc, s), "k_add (preprocess)");
+    }
+    for (int b = 0; b < B && Mt; b++)
+        STEP(hipMemcpyAsync(h->dseq + (size_t)b * S * E, h->mem, (size_t)Mt * E * 4, hipMemcpyDeviceToDevice, s),
+             "memory tokens");
+    STEP(aria_k_sgemm(h->dseq + (size_t)Mt * E, h->dxtc, h->pin, NULL, T, E, C, 1, 1.0f, B, (long long)T * C, 0,
+                      (long long)S * E, s), "project_in");
+    for (int b = 0; b < h->depth; b++) {
+        int rc = block_forward(h->blk[b], h->dseq, B, S, h->dgcond, h->ck[b], h->cv[b], h->Sc, h->cos_t, h->sin_t,
+                               h->rot, h->local ? h->local[b] : NULL, h->ws, h->ws_bytes, s);
+        if (rc) return rc;
+    }
+    STEP(aria_k_sgemm(h->dout, h->dseq + (size_t)Mt * E, h->pout, NULL, T, C, E, 1, 1.0f, B, (long long)S * E, 0,
+                      (long long)T * C, s), "project_out");
+    if (h->post) {
+        STEP(aria_k_sgemm(h->dtmp, h->dout, h->post, NULL, B * T, C, C, 1, 1.0f, 1, 0, 0, 0, s), "postprocess");
+        STEP(aria_k_add(h->dout, h->dout, h->dtmp, nxc, s), "k_add (postprocess)");
+    }
+    STEP(aria_k_transpose(h->dv, h->dout, T, C, B, s), "k_transpose (v)");
+    return 0;
+}
+
+/* run one step: replay the captured graph, capturing it on first use (ARIA_NO_GRAPH=1 when the
+ * handle was created, or a failed capture -> inline; the reference's policy,
+ * src/aria_cuda.cu:1450-1489) */
+static int dit_run(aria_cuda_dit *h, hipStream_t s) {
+    if (h->no_graph) h->graph_failed = 1;
+    if (h->graph_ready) {
+        hipError_t e = hipGraphLaunch(h->gexec, s);
+        return e == hipSuccess ? 0 : FAIL(e, "hipGraphLaunch");
+    }
+    if (h->graph_failed) return step_compute(h, s);
+    hipStreamSynchronize(s);
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+        hipGetLastError();
+        h->graph_failed = 1;
+        return step_compute(h, s);
+    }
+    int rc = step_compute(h, s);
+    hipGraph_t g = NULL;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (!rc && e == hipSuccess && g && hipGraphInstantiate(&h->gexec, g, NULL, NULL, 0) == hipSuccess) {
+        h->graph = g;
+        h->graph_ready = 1;
+        e = hipGraphLaunch(h->gexec, s);
+        return e == hipSuccess ? 0 : FAIL(e, "hipGraphLaunch");
+    }
+    hipGetLastError();
+    if (g) hipGraphDestroy(g);
+    h->graph_failed = 1;
+    return step_compute(h, s);   /* capture failed: run inline (correctness preserved) */
+}
+
+int aria_hip_dit_graph_active(const aria_cuda_dit *h) { return h && h->graph_ready; }
+
+int aria_hip_dit_device_buffers(aria_cuda_dit *h, float **dx, float **dv, float **dgcond) {
+    if (!h || !h->have_req) return ARIA_HIP_EINVAL;
+    if (dx) *dx = h->dx;
+    if (dv) *dv = h->dv;
+    if (dgcond) *dgcond = h->dgcond;
+    return 0;
+}
+
+int aria_hip_dit_run(aria_cuda_dit *h, void *stream) {
+    int rc = aria_hip_ensure();
+    if (rc) return rc;
+    if (!h || !h->have_req) { aria_hip_set_error("aria_hip_dit_run: no request set"); return ARIA_HIP_EINVAL; }
+    return dit_run(h, stream ? (hipStream_t)stream : h->st);
+}
+
+int aria_hip_dit_step_batch(aria_cuda_dit *h, float *v, const float *x, const float *gcond) {
+    int rc = aria_hip_ensure();
+    if (rc) return rc;
+    if (!h || !h->have_req || !v || !x || !gcond) {
+        aria_hip_set_error("aria_hip_dit_step_batch: no request set or NULL buffer");
+        return ARIA_HIP_EINVAL;
+    }
+    const size_t n = (size_t)h->B * h->io_ch * h->T, ng = (size_t)h->B * 6 * h->ed;
+    STEP(hipMemcpyAsync(h->dx, x, n * 4, hipMemcpyHostToDevice, h->st), "hipMemcpyAsync (x)");
+    STEP(hipMemcpyAsync(h->dgcond, gcond, ng * 4, hipMemcpyHostToDevice, h->st), "hipMemcpyAsync (gcond)");
+    rc = dit_run(h, h->st);
+    if (rc) return rc;
+    STEP(hipMemcpyAsync(v, h->dv, n * 4, hipMemcpyDeviceToHost, h->st), "hipMemcpyAsync (v)");
+    STEP(hipStreamSynchronize(h->st), "hipStreamSynchronize");
+    return 0;
+}
+
+void aria_cuda_dit_step(aria_cuda_dit *h, float *v_CT, const float *x_CT, const float *gcond) {
+    if (h && h->B != 1) { aria_hip_set_error("aria_cuda_dit_step: request has %d sequences", h->B); return; }
+    aria_hip_dit_step_batch(h, v_CT, x_CT, gcond);
+}
+
+static int pin_grow(float **p, size_t *cap, size_t n) {
+    if (n <= *cap) return 0;
+    if (*p) hipHostFree(*p);
+    *p = NULL; *cap = 0;
+    if (hipHostMalloc((void **)p, n * sizeof(float), 0) != hipSuccess) { hipGetLastError(); *p = NULL; return -1; }
+    *cap = n;
+    return 0;
+}
+
+int aria_cuda_dit_sample(aria_cuda_dit *h, float *x_CT, const float *sched, int steps, const float *gcond_all,
+                         void (*noise)(float *, int, void *), void *noise_user, void (*progress)(int, int, void *),
+                         void *progress_user) {
+    if (aria_hip_ensure() || !h || !h->have_req || !x_CT || !sched || !gcond_all || !noise || steps < 0) return -1;
+    const size_t n = (size_t)h->B * h->io_ch * h->T, ng = (size_t)h->B * 6 * h->ed;
+    hipStream_t st = h->st;
+    if (pin_grow(&h->pin_gc, &h->pin_gc_n, (size_t)(steps ? steps : 1) * ng)) return -1;
+    if (h->pin_nz_n < n) {   /* the two noise buffers grow together */
+        size_t c0 = 0, c1 = 0;
+        h->pin_nz_n = 0;
+        if (pin_grow(&h->pin_nz[0], &c0, n) || pin_grow(&h->pin_nz[1], &c1, n)) return -1;
+        h->pin_nz_n = n;
+    }
+    memcpy(h->pin_gc, gcond_all, (size_t)steps * ng * sizeof(float));
+    hipEvent_t ev_nz[2], ev_step;
+    hipEventCreateWithFlags(&ev_nz[0], hipEventDisableTiming);
+    hipEventCreateWithFlags(&ev_nz[1], hipEventDisableTiming);
+    hipEventCreateWithFlags(&ev_step, hipEventDisableTiming);
+    int rc = 0;
+    if (hipMemcpyAsync(h->dx, x_CT, n * 4, hipMemcpyHostToDevice, st) != hipSuccess) rc = -1;
+    for (int i = 0; i < steps && !rc; i++) {
+        h->cur_step = i;
+        if (hipMemcpyAsync(h->dgcond, h->pin_gc + (size_t)i * ng, ng * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+            dit_run(h, st)) { rc = -1; break; }
+        const int b = i & 1;
+        if (i >= 2) hipEventSynchronize(ev_nz[b]);      /* step i-2's upload from this buffer is done */
+        noise(h->pin_nz[b], (int)n, noise_user);         /* drawn on the host while the step runs */
+        if (hipMemcpyAsync(h->dnoise, h->pin_nz[b], n * 4, hipMemcpyHostToDevice, st) != hipSuccess) { rc = -1; break; }
+        hipEventRecord(ev_nz[b], st);
+        if (aria_k_pingpong(h->dx, h->dv, h->dnoise, sched[i], sched[i + 1], n, st) != hipSuccess) { rc = -1; break; }
+        if (progress) {
+            hipEventRecord(ev_step, st);
+            hipEventSynchronize(ev_step);
+            progress(i + 1, steps, progress_user);
+        }
+    }
+    if (!rc && hipMemcpyAsync(x_CT, h->dx, n * 4, hipMemcpyDeviceToHost, st) != hipSuccess) rc = -1;
+    if (hipStreamSynchronize(st) != hipSuccess) rc = -1;
+    hipEventDestroy(ev_nz[0]); hipEventDestroy(ev_nz[1]); hipEventDestroy(ev_step);
+    return rc;
+}
+
+/* ------------------------------------------------------------------------- */
+/* device decoders: not served here; NULL keeps the caller on its CPU decoder */
+/* ------------------------------------------------------------------------- */
+
+aria_cuda_dec *aria_cuda_dec_create(const aria_sa3_dec_view *v) {
+    (void)v;
+    aria_hip_set_error("aria_cuda_dec_create: the device decoder is not part of this backend");
+    return NULL;
+}
+void aria_cuda_dec_free(aria_cuda_dec *h) { (void)h; }
+void aria_cuda_dec_forward(aria_cuda_dec *h, float *audio, const float *latent, int T) {
+    (void)h; (void)audio; (void)latent; (void)T;
+    aria_hip_set_error("aria_cuda_dec_forward: no device decoder");
+}
+aria_cuda_dec_medium *aria_cuda_dec_medium_create(const aria_sa3_dec_medium_view *v) {
+    (void)v;
+    aria_hip_set_error("aria_cuda_dec_medium_create: the device decoder is not part of this backend");
+    return NULL;
+}
+void aria_cuda_dec_medium_free(aria_cuda_dec_medium *h) { (void)h; }
+void aria_cuda_dec_medium_forward(aria_cuda_dec_medium *h, float *audio, const float *latent, int T) {
+    (void)h; (void)audio; (void)latent; (void)T;
+    aria_hip_set_error("aria_cuda_dec_medium_forward: no device decoder");
 }

@@ -55,6 +55,8 @@ hipError_t aria_k_pingpong(float *x, const float *v, const float *noise, float t
                            size_t n, hipStream_t s);
 /* fp32 -> fp16 (RTNE), n elements. */
 hipError_t aria_k_f32_to_f16(uint16_t *y, const float *x, size_t n, hipStream_t s);
+/* per batch b: dst[b] [cols, rows] = transpose of src[b] [rows, cols] */
+hipError_t aria_k_transpose(float *dst, const float *src, int rows, int cols, int batch, hipStream_t s);
 /* mod[c][b][i] = tssg[c*dim+i] + gcond[b*6*dim + c*dim + i] (gcond may be NULL), c < 6 */
 hipError_t aria_k_mod_chunks(float *mod, const float *tssg, const float *gcond, int B, int dim,
                              hipStream_t s);

@@ -291,6 +291,30 @@ extern "C" hipError_t aria_k_pingpong(float *x, const float *v, const float *noi
     return hipGetLastError();
 }
 
+/* batched 2-D transpose through a 32x33 LDS tile: dst[b][c][r] = src[b][r][c]
+ * (the DiT step's [C,T] <-> [T,C] latent reshapes, src/aria_sa3_dit.c:585-597) */
+__global__ __launch_bounds__(256) void k_transpose(float *dst, const float *src, int rows, int cols) {
+    __shared__ float t[32][33];
+    const size_t base = (size_t)blockIdx.z * rows * cols;
+    const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   /* 32 x 8 threads */
+    for (int i = ty; i < 32; i += 8) {
+        const int r = r0 + i, c = c0 + tx;
+        if (r < rows && c < cols) t[i][tx] = src[base + (size_t)r * cols + c];
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const int c = c0 + i, r = r0 + tx;
+        if (r < rows && c < cols) dst[base + (size_t)c * rows + r] = t[tx][i];
+    }
+}
+extern "C" hipError_t aria_k_transpose(float *dst, const float *src, int rows, int cols, int batch, hipStream_t s) {
+    if (rows <= 0 || cols <= 0 || batch <= 0) return hipSuccess;
+    dim3 grid((cols + 31) / 32, (rows + 31) / 32, batch);
+    hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, s, dst, src, rows, cols);
+    return hipGetLastError();
+}
+
 /* DiT modulation (src/aria_sa3_dit.c:152-156): mod = to_scale_shift_gate + gcond[b],
  * written chunk-major mod[c][b][i] (c < 6) so each of the six [B, dim] slices
  * (scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff) is contiguous. */

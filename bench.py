@@ -59,6 +59,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (cache defeat)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-dit", action="store_true", help="skip the 24-block DiT stack leg")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: each C2 op a few times with no events in between, plus one "
                          "256 MiB device-to-device copy whose FETCH/WRITE counters calibrate the others")
@@ -267,6 +268,8 @@ def main():
     del sets
     # C4: one q4 DiT block at T = 1296, batch 2
     block = block_leg(DeviceArray, time_loop, stream, rng, reps)
+    # C5: 24-block q4 stack x 8 steps, graph replay vs inline, and the device sampler
+    dit = None if args.no_dit else dit_leg(DeviceArray, Timer, L, chk, stream, rng)
 
     dom = max(OPS, key=lambda o: ops_report[o]["us"])
     dom_us = ops_report[dom]["us"]
@@ -299,6 +302,7 @@ def main():
         "gemm": gemm,
         "block_us": block["gelu"]["us"],
         "block": block,
+        "dit": dit,
         "wall_s_timed": round(t_wall, 3),
     }
     print(json.dumps(line), flush=True)
@@ -364,6 +368,61 @@ def block_leg(DeviceArray, time_loop, stream, rng, reps):
         out[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "flop": flop,
                      "weight_bytes": blk.weight_bytes}
         blk.free()
+    return out
+
+
+def dit_leg(DeviceArray, Timer, L, chk, stream, rng, steps=8, depth=24):
+    """Config 5: a 24-block random-init q4 DiT stack (config-4 block shape, tanh-GELU 4x FFN, one
+    seed stream for all blocks) at T = 1296, batch 2 (the CFG pair as one batched request),
+    latent [2, 64, 1296] ~N(0,1), project_in [1024,64], project_out [64,1024], pre/post 1x1
+    convs [64,64]; context embeddings [2, 256, 1024] ~N(0,1) (cross K/V projected once per
+    request, outside the timing); per-step gcond [2, 6*1024] ~N(0,0.1). Timed: 8 device-resident
+    steps (aria_hip_dit_run) replaying the captured graph, the same with the graph off, and the
+    whole 8-step pingpong sampler (aria_cuda_dit_sample: host noise + H2D each step)."""
+    from aria_amd.dit import Dit, random_dit, FFN_GELU, Q4
+    Bb, T, C, ed, H, inner, Sc = B, S, 64, 1024, 16, 4096, 256
+    M = random_dit(rng, depth, ed, inner, C, 0, ffn=FFN_GELU)
+    inv = 1.0 / (10000.0 ** (np.arange(16) * 2.0 / 32))
+    ang = np.arange(T)[:, None] * inv[None, :]
+    cos32, sin32 = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    ced = [rng.standard_normal((Sc, ed), dtype=np.float32) for _ in range(Bb)]
+    x0 = rng.standard_normal((Bb, C, T), dtype=np.float32)
+    gall = (0.1 * rng.standard_normal((steps, Bb, 6 * ed))).astype(np.float32)
+    sched = np.linspace(1.0, 0.0, steps + 1).astype(np.float32)
+    out = {"depth": depth, "T": T, "batch": Bb, "io_ch": C, "steps": steps, "ffn": "gelu4x", "precision": "q4"}
+    for mode in ("graph", "inline"):
+        if mode == "inline":
+            os.environ["ARIA_NO_GRAPH"] = "1"
+        try:
+            dit = Dit(M, depth, ed, H, inner, C, 0, 32, precision=Q4, ffn=FFN_GELU)
+        finally:
+            os.environ.pop("ARIA_NO_GRAPH", None)
+        dit.set_request(T, ced, cos32, sin32)
+        dx, dv, dg = dit.device_buffers()
+        L.aria_cuda_memcpy_h2d(dx, x0.ctypes.data, x0.nbytes)
+        d_g = [DeviceArray.from_host(gall[i]) for i in range(steps)]
+        L.aria_cuda_memcpy_h2d(dg, gall[0].ctypes.data, gall[0].nbytes)
+        dit.run(stream)                      # first step captures the graph (graph mode)
+        chk(L.aria_hip_stream_sync(stream))
+        tm = Timer(stream)
+        tm.start()
+        for i in range(steps):
+            chk(L.aria_hip_memcpy_d2d_async(dg, d_g[i].p, d_g[i].nbytes, stream))
+            dit.run(stream)
+        out[f"{mode}_ms_per_step"] = round(tm.stop() / steps, 3)
+        if mode == "graph":
+            out["graph_active"] = dit.graph_active
+            nz = np.random.default_rng(SEED + 5)
+            t0 = time.perf_counter()
+            dit.sample(x0, sched, gall.reshape(steps, -1), lambda n: nz.standard_normal(n, dtype=np.float32))
+            out["sample_ms_8steps"] = round((time.perf_counter() - t0) * 1e3, 1)
+        dit.free()
+        del d_g
+    blk = 2.0 * Bb * T * ed * (6 * ed) + 2.0 * Bb * T * ed * (2 * inner) \
+        + 2 * 2.0 * Bb * H * T * T * 64 + 2 * 2.0 * Bb * H * T * Sc * 64
+    flop = depth * blk + 2 * 2.0 * Bb * T * C * ed + 2 * 2.0 * Bb * T * C * C
+    out["flop_per_step"] = flop
+    out["TFLOP/s_graph"] = round(flop / (out["graph_ms_per_step"] * 1e-3) / 1e12, 1)
     return out
 
 

@@ -93,6 +93,105 @@ int aria_hip_dit_block_forward_dev(aria_hip_dit_block *b, float *dx, int B, int 
                                    const uint16_t *dk, const uint16_t *dv, int Sc, const float *dcos,
                                    const float *dsin, int rot, void *dws, size_t ws_bytes, void *stream);
 
+/* ------------------------------------------------------------------------- */
+/* The reference's device-resident DiT ABI (src/aria_sa3_dit.h:127-171)      */
+/* ------------------------------------------------------------------------- */
+
+#ifndef ARIA_STEER_H
+/* src/aria_steer.h:14-38 (steering is accepted; this backend does not apply it) */
+typedef enum { ARIA_STEER_RESIDUAL = 0, ARIA_STEER_LATENT, ARIA_STEER_COND } aria_steer_site;
+typedef enum { ARIA_STEER_ADD = 0, ARIA_STEER_PROJECT } aria_steer_op;
+typedef struct {
+    aria_steer_site site;
+    aria_steer_op op;
+    int layer;
+    const float *dir;
+    int dim;
+    float dir_norm2;
+    float scale;
+    int step_lo, step_hi;
+} aria_steer;
+typedef struct { const aria_steer *items; int n; } aria_steer_set;
+#endif
+
+#ifndef ARIA_SA3_DIT_H
+/* src/aria_sa3_dit.h:128-133 */
+typedef struct {
+    int depth, ed, num_heads, head_dim, inner, io_ch, n_mem, rot_dim;
+    int differential;
+    const float *preprocess, *postprocess, *project_in, *project_out, *memory_tokens;
+    const aria_dit_block_w *blocks;
+} aria_sa3_dit_view;
+/* src/aria_sa3_dit.h:136-145 */
+typedef struct {
+    int T, S, n_cond, depth;
+    const float *global_seconds, *rope_cos, *rope_sin;
+    float *const *cross_k, *const *cross_v;
+    float *const *cross_kd;
+    const float *cross_ed;
+    float *const *local_emb;
+    int has_local;
+    const aria_steer_set *steer;
+} aria_sa3_dit_req_view;
+typedef struct aria_cuda_dit aria_cuda_dit;
+#endif
+
+/* src/aria_sa3_dit.h:155 - upload the model (SiLU-GLU blocks, ca_to_kv [2*ed, ed]) packed
+ * per precision (see aria_hip_dit_block_create). NULL when there is no device, the shape
+ * is unsupported (differential attention, head_dim != 64) or it does not fit; the
+ * reference's caller then runs the CPU DiT (src/aria_model_sa3.c:503-509). */
+aria_cuda_dit *aria_cuda_dit_create(const aria_sa3_dit_view *v, aria_dtype precision);
+/* src/aria_sa3_dit.h:156 */
+void aria_cuda_dit_free(aria_cuda_dit *h);
+/* src/aria_sa3_dit.h:157 - per request: cross K/V of every block from cross_ed (projected on
+ * the device), RoPE tables, local-additive cond; copies what it needs (steer is borrowed). */
+void aria_cuda_dit_set_request(aria_cuda_dit *h, const aria_sa3_dit_req_view *rv);
+/* src/aria_sa3_dit.h:159 - current denoise step (steering window; kept for the ABI) */
+void aria_cuda_dit_set_step(aria_cuda_dit *h, int step);
+/* src/aria_sa3_dit.h:161 - v_CT = velocity(x_CT, gcond), [io_ch, T] host buffers, gcond [6*ed];
+ * synchronous. The step runs as one captured HIP graph after its first call
+ * (ARIA_NO_GRAPH=1 forces the inline path). */
+void aria_cuda_dit_step(aria_cuda_dit *h, float *v_CT, const float *x_CT, const float *gcond);
+/* src/aria_sa3_dit.h:167-171 - the pingpong sampler with x resident on the device; gcond_all
+ * [steps][6*ed], noise(buf, n, user) called once per step in order; bit-identical to
+ * aria_cuda_dit_step + the host pingpong update. -1 (nothing run) if pinned staging fails. */
+int aria_cuda_dit_sample(aria_cuda_dit *h, float *x_CT, const float *sched, int steps,
+                         const float *gcond_all, void (*noise)(float *, int, void *), void *noise_user,
+                         void (*progress)(int, int, void *), void *progress_user);
+
+/* aria_cuda_dit_create with the FFN form chosen: ARIA_FFN_GLU (the SA3 model, what
+ * aria_cuda_dit_create builds) or ARIA_FFN_GELU (a tanh-GELU MLP, ff_in_w [inner, ed]). */
+aria_cuda_dit *aria_hip_dit_create_ex(const aria_sa3_dit_view *v, aria_dtype precision, int ffn);
+
+/* ---- batched extension: B sequences (the CFG pair) per pass over the weights ---- */
+/* rv: B request views with equal T and n_cond (one cross_ed each). */
+int aria_hip_dit_set_request_batch(aria_cuda_dit *h, const aria_sa3_dit_req_view *rv, int B);
+/* host buffers: v, x [B, io_ch, T]; gcond [B, 6*ed]; synchronous */
+int aria_hip_dit_step_batch(aria_cuda_dit *h, float *v, const float *x, const float *gcond);
+/* The handle's device step buffers (x [B, io_ch, T] in, v out, gcond [B, 6*ed]) and one
+ * stream-ordered step on them (graph replay after the first call), for callers that keep
+ * the latent in HBM; stream NULL = the handle's stream. */
+int aria_hip_dit_device_buffers(aria_cuda_dit *h, float **dx, float **dv, float **dgcond);
+int aria_hip_dit_run(aria_cuda_dit *h, void *stream);
+/* 1 if the step runs as a captured graph, 0 if inline */
+int aria_hip_dit_graph_active(const aria_cuda_dit *h);
+
+/* ---- device decoders (src/aria_sa3_dec.h:98-109): not served by this backend ----
+ * create returns NULL (no fit), so the reference's caller keeps its CPU decoder
+ * (src/aria_model_sa3.c:293-305, 634-647); free and forward accept only that NULL. */
+#ifndef ARIA_SA3_DEC_H
+typedef struct aria_sa3_dec_view aria_sa3_dec_view;
+typedef struct aria_sa3_dec_medium_view aria_sa3_dec_medium_view;
+typedef struct aria_cuda_dec aria_cuda_dec;
+typedef struct aria_cuda_dec_medium aria_cuda_dec_medium;
+aria_cuda_dec *aria_cuda_dec_create(const aria_sa3_dec_view *v);
+void aria_cuda_dec_free(aria_cuda_dec *h);
+void aria_cuda_dec_forward(aria_cuda_dec *h, float *audio, const float *latent, int T);
+aria_cuda_dec_medium *aria_cuda_dec_medium_create(const aria_sa3_dec_medium_view *v);
+void aria_cuda_dec_medium_free(aria_cuda_dec_medium *h);
+void aria_cuda_dec_medium_forward(aria_cuda_dec_medium *h, float *audio, const float *latent, int T);
+#endif
+
 #ifdef __cplusplus
 }
 #endif

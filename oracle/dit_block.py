@@ -69,8 +69,10 @@ def cross_kv(ops, ctx, W, H, ca_kv=None):
     return k, v
 
 
-def block_forward(ops, P, x, kc, vc, gcond, W, packed, cos_t, sin_t, rot, H, ffn=FFN_GLU):
-    """One block on one sequence: x [S, dim] -> new x. kc/vc [H, Sc, 64] from cross_kv."""
+def block_forward(ops, P, x, kc, vc, gcond, W, packed, cos_t, sin_t, rot, H, ffn=FFN_GLU, local=None):
+    """One block on one sequence: x [S, dim] -> new x. kc/vc [H, Sc, 64] from cross_kv.
+    local: the inpaint local-additive cond [S, dim] added after the cross-attention
+    residual (src/aria_sa3_dit.c:247-252), or None."""
     S, dim = x.shape
 
     def lin(name, h, bias=None):
@@ -103,6 +105,8 @@ def block_forward(ops, P, x, kc, vc, gcond, W, packed, cos_t, sin_t, rot, H, ffn
     qc = ops.rmsnorm(qc.reshape(-1, 64), W["ca_q_norm"], 1e-6).reshape(qc.shape)
     o = lin("ca_to_out", merge(ops.attention(qc, kc, vc)))
     x = ops.add(x, o)
+    if local is not None:
+        x = ops.add(x, np.ascontiguousarray(local, np.float32))
     # feed-forward
     h = ops.rmsnorm(x, W["ff_norm"], 1e-5)
     h = P.adaln_modulate(h, sc_f, sh_f)

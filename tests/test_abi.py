@@ -83,6 +83,11 @@ def test_no_device_behaviour(libpath):
     assert L.aria_hip_rmsnorm_dev(None, None, None, 1, 8, 1e-6, None) == -2
     assert "no HIP device" in aria_amd.last_error()
     assert aria_amd.device_info() == "no HIP device"
+    # the DiT and decoder handles: NULL, so the reference's caller keeps its CPU path
+    assert not L.aria_cuda_dit_create(None, 4)
+    assert not L.aria_cuda_dec_create(None)
+    assert not L.aria_cuda_dec_medium_create(None)
+    assert L.aria_hip_dit_set_request_batch(None, None, 2) == -2
 
 
 def test_oracle_is_not_linked_into_product(libpath):
@@ -91,3 +96,27 @@ def test_oracle_is_not_linked_into_product(libpath):
     assert "oracle" not in out and "aria_ref" not in out
     exp = exported_symbols(libpath)
     assert not [s for s in exp if s.startswith("or_")]
+
+
+def test_struct_layouts(tmp_path):
+    """The restated reference types are byte-compatible: sizes and offsets as the reference
+    headers give them on x86-64 (src/aria_sa3_dit.h:40-48, 128-145, src/aria_steer.h:26-38)."""
+    src = tmp_path / "layout.c"
+    src.write_text("""
+#include <stdio.h>
+#include <stddef.h>
+#include "aria_dit.h"
+int main(void) {
+    printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n",
+           sizeof(aria_dit_block_w), sizeof(aria_sa3_dit_view), offsetof(aria_sa3_dit_view, blocks),
+           sizeof(aria_sa3_dit_req_view), offsetof(aria_sa3_dit_req_view, cross_ed),
+           offsetof(aria_sa3_dit_req_view, steer), sizeof(aria_steer), sizeof(aria_steer_set),
+           offsetof(aria_sa3_dit_req_view, has_local), sizeof(aria_dtype));
+    return 0;
+}
+""")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got == [168, 88, 80, 96, 64, 88, 48, 16, 80, 4]

@@ -1,0 +1,274 @@
+"""GPU parity of the device-resident DiT (the reference's aria_cuda_dit_* ABI, include/aria_dit.h).
+
+Oracle, per sequence: the reference's own step composition (src/aria_sa3_dit.c:734-777) on the
+CPU -- transpose, preprocess_conv + x, memory tokens + project_in, the depth blocks through the
+compiled reference's aria_dit_block_forward on the dequantized weights (what dequant-on-use
+computes), project_out, postprocess_conv + out, transpose -- with the reference's linear.
+Gate: the reference's full-DiT gate, max|d| <= 2e-3 + 5e-3 * max|ref| (tests/test_dit_full.c:61).
+
+The sampler is checked bit-exact against aria_cuda_dit_step + the host pingpong update, the
+reference's own contract for aria_cuda_dit_sample (src/aria_sa3_dit.h:163-166); the captured
+graph bit-exact against the inline step, over several replays with host work in between.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, randn, rng
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 5e-3
+PNAME = {4: "q4", 3: "q8", 0: "f32"}
+
+
+@pytest.fixture
+def R(ref):
+    if ref is None:
+        pytest.skip("oracle/_ref not built: the DiT oracle needs the compiled reference")
+    return ref
+
+
+def model(seed, depth=2, ed=128, inner=256, io_ch=16, n_mem=3):
+    from aria_amd.dit import random_dit
+    return random_dit(rng(seed), depth, ed, inner, io_ch, n_mem)
+
+
+def make_dit(M, precision, H=2, rot=32):
+    from aria_amd.dit import Dit
+    ed = M["project_in"].shape[0]
+    return Dit(M, len(M["blocks"]), ed, H, M["blocks"][0]["ff_out_w"].shape[1], M["project_in"].shape[1],
+               M["memory_tokens"].shape[0], rot, precision=precision)
+
+
+def ref_step(R, port, M, precision, x_CT, ced, gcond, c, s, rot, H, local=None, ffn=0):
+    """velocity of one sequence on the CPU, src/aria_sa3_dit.c:734-777. SiLU-GLU blocks run the
+    reference's aria_dit_block_forward; tanh-GELU blocks the pinned composition of reference ops,
+    both on the dequantized weights with the reference's fp32 linear."""
+    from oracle import dit_block as DB
+    n_mem, ed = M["memory_tokens"].shape
+    inner = M["blocks"][0]["ff_out_w"].shape[1]
+    xtc = np.ascontiguousarray(x_CT.T)
+    xtc = xtc + R.linear(xtc, M["preprocess"])
+    seq = np.concatenate([M["memory_tokens"], R.linear(xtc, M["project_in"])]).astype(np.float32)
+    for b, W in enumerate(M["blocks"]):
+        packed = DB.pack_weights(R, W, PNAME[precision])
+        if ffn == DB.FFN_GELU:
+            Wd = DB.dequantized(port, W, packed)
+            kc, vc = DB.cross_kv(R, ced, W, H)
+            seq = DB.block_forward(R, port, seq, kc, vc, gcond, Wd, DB.pack_weights(R, Wd, "f32"), c, s, rot, H,
+                                   DB.FFN_GELU)
+        elif local is None:
+            seq = R.dit_block_forward(seq, ced, gcond, c, s, rot, DB.dequantized(port, W, packed), H, inner)
+        else:
+            kc, vc = DB.cross_kv(R, ced, W, H)
+            seq = DB.block_forward(R, port, seq, kc, vc, gcond, W, packed, c, s, rot, H, DB.FFN_GLU, local[b])
+    out = R.linear(np.ascontiguousarray(seq[n_mem:]), M["project_out"])
+    out = out + R.linear(out, M["postprocess"])
+    return np.ascontiguousarray(out.T)
+
+
+def inputs(seed, B, io_ch, T, n_cond, ed):
+    r = rng(seed)
+    return randn(r, (B, io_ch, T)), randn(r, (B, n_cond, ed)), randn(r, (B, 6 * ed), 0.1)
+
+
+@pytest.mark.parametrize("precision", [4, 3, 0])        # ARIA_Q4, ARIA_Q8, ARIA_F32 (fp16 storage)
+def test_dit_step_parity(hip, port, R, precision):
+    """aria_cuda_dit_step, batch 1, two teacher-forced steps on one request."""
+    M = model(11 + precision)
+    T, n_cond, H, rot = 40, 12, 2, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = R.rope_freqs(S, rot, 10000.0)
+    dit = make_dit(M, precision, H, rot)
+    _, ced, _ = inputs(1, 1, io_ch, T, n_cond, ed)
+    dit.set_request(T, [ced[0]], c, s)
+    for k in range(2):
+        x, _, g = inputs(100 + k, 1, io_ch, T, n_cond, ed)
+        got = dit.step(x, g)
+        want = ref_step(R, port, M, precision, x[0], ced[0], g[0], c, s, rot, H)
+        assert_close(got[0], want, ATOL, RTOL, f"dit step {k} {PNAME[precision]}")
+    dit.free()
+
+
+def test_dit_batch_cfg_pair(hip, port, R):
+    """aria_hip_dit_set_request_batch / step_batch: the CFG pair (two contexts) in one pass."""
+    M = model(21)
+    T, n_cond, H, rot = 33, 9, 2, 64
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = R.rope_freqs(S, rot, 10000.0)
+    dit = make_dit(M, 4, H, rot)
+    x, ced, g = inputs(2, 2, io_ch, T, n_cond, ed)
+    dit.set_request(T, [ced[0], ced[1]], c, s)
+    got = dit.step(x, g)
+    for b in range(2):
+        want = ref_step(R, port, M, 4, x[b], ced[b], g[b], c, s, rot, H)
+        assert_close(got[b], want, ATOL, RTOL, f"cfg pair seq {b}")
+    dit.free()
+
+
+def test_dit_local_cond(hip, port, R):
+    """inpaint local-additive cond: added per block after the cross-attention residual."""
+    M = model(31)
+    T, n_cond, H, rot = 24, 8, 2, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    n_mem = M["memory_tokens"].shape[0]
+    S = n_mem + T
+    c, s = R.rope_freqs(S, rot, 10000.0)
+    r = rng(5)
+    local = []
+    for _ in M["blocks"]:
+        a = np.zeros((S, ed), np.float32)
+        a[n_mem:] = randn(r, (T, ed), 0.5)    # zeros at the memory-token rows, as the reference pads
+        local.append(a)
+    dit = make_dit(M, 4, H, rot)
+    x, ced, g = inputs(3, 1, io_ch, T, n_cond, ed)
+    dit.set_request(T, [ced[0]], c, s, local=[local])
+    got = dit.step(x, g)
+    want = ref_step(R, port, M, 4, x[0], ced[0], g[0], c, s, rot, H, local=local)
+    assert_close(got[0], want, ATOL, RTOL, "dit local cond")
+    # planted check: the same step without the local cond must differ beyond the gate
+    plain = ref_step(R, port, M, 4, x[0], ced[0], g[0], c, s, rot, H)
+    assert np.abs(plain - want).max() > ATOL + RTOL * np.abs(want).max()
+    dit.free()
+
+
+def test_dit_host_projected_kv(hip, port, R):
+    """legacy request form: no cross_ed, per-block host K/V [H, n_cond, 64] (fp32 -> fp16 on upload)."""
+    from oracle import dit_block as DB
+    M = model(41)
+    T, n_cond, H, rot = 20, 10, 2, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = R.rope_freqs(S, rot, 10000.0)
+    x, ced, g = inputs(4, 1, io_ch, T, n_cond, ed)
+    ks, vs = [], []
+    for W in M["blocks"]:
+        k, v = DB.cross_kv(R, ced[0], W, H)
+        ks.append(k); vs.append(v)
+    dit = make_dit(M, 4, H, rot)
+    dit.set_request(T, [None], c, s, cross_kv=[(ks, vs)])
+    got = dit.step(x, g)
+    want = ref_step(R, port, M, 4, x[0], ced[0], g[0], c, s, rot, H)
+    assert_close(got[0], want, ATOL, RTOL, "dit host K/V")
+    dit.free()
+
+
+def test_dit_graph_matches_inline(hip, port, monkeypatch):
+    """the captured step replays bit-identically to the inline step (ARIA_NO_GRAPH=1), across
+    several replays with fresh inputs and host work in between; a warm-hit set_request
+    (same context) keeps the graph."""
+    M = model(51)
+    T, n_cond, H, rot = 36, 8, 2, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = port.rope_freqs(S, rot, 10000.0)
+    _, ced, _ = inputs(6, 2, io_ch, T, n_cond, ed)
+    monkeypatch.setenv("ARIA_NO_GRAPH", "1")
+    inline = make_dit(M, 4, H, rot)
+    inline.set_request(T, [ced[0], ced[1]], c, s)
+    monkeypatch.delenv("ARIA_NO_GRAPH")
+    graph = make_dit(M, 4, H, rot)
+    graph.set_request(T, [ced[0], ced[1]], c, s)
+    for k in range(3):
+        x, _, g = inputs(200 + k, 2, io_ch, T, n_cond, ed)
+        a = inline.step(x, g)
+        b = graph.step(x, g)
+        assert not inline.graph_active
+        assert graph.graph_active, "the step was not captured"
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"replay {k} differs from inline"
+        np.sum(a * 1.0001)   # host work between replays
+    graph.set_request(T, [ced[0], ced[1]], c, s)   # warm hit
+    assert graph.graph_active
+    x, _, g = inputs(300, 2, io_ch, T, n_cond, ed)
+    assert np.array_equal(inline.step(x, g).view(np.uint32), graph.step(x, g).view(np.uint32))
+    inline.free(); graph.free()
+
+
+def test_dit_device_buffers_run(hip, port):
+    """aria_hip_dit_device_buffers + aria_hip_dit_run: the step on HBM-resident buffers equals
+    the host-buffer step bit for bit."""
+    from aria_amd import lib
+    M = model(61)
+    T, n_cond, H, rot = 28, 8, 2, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = port.rope_freqs(S, rot, 10000.0)
+    x, ced, g = inputs(7, 1, io_ch, T, n_cond, ed)
+    dit = make_dit(M, 4, H, rot)
+    dit.set_request(T, [ced[0]], c, s)
+    want = dit.step(x, g)
+    dx, dv, dg = dit.device_buffers()
+    L = lib()
+    L.aria_cuda_memcpy_h2d(dx, x.ctypes.data, x.nbytes)
+    L.aria_cuda_memcpy_h2d(dg, g.ctypes.data, g.nbytes)
+    dit.run()
+    L.aria_cuda_sync()
+    got = np.empty_like(x)
+    L.aria_cuda_memcpy_d2h(got.ctypes.data, dv, got.nbytes)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    dit.free()
+
+
+def test_dit_sample_bitexact(hip, port):
+    """aria_cuda_dit_sample == aria_cuda_dit_step + the host pingpong update, bit for bit,
+    with the noise drawn in the same order."""
+    M = model(71)
+    T, n_cond, H, rot, steps = 30, 8, 2, 32, 5
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = port.rope_freqs(S, rot, 10000.0)
+    x0, ced, _ = inputs(8, 1, io_ch, T, n_cond, ed)
+    gall = randn(rng(9), (steps, 6 * ed), 0.1)
+    sched = np.linspace(1.0, 0.0, steps + 1).astype(np.float32)
+    dit = make_dit(M, 4, H, rot)
+    dit.set_request(T, [ced[0]], c, s)
+
+    def noise_stream(seed):
+        r = rng(seed)
+        return lambda n: r.standard_normal(n).astype(np.float32)
+
+    seen = []
+    got = dit.sample(x0[0], sched, gall, noise_stream(10), progress=lambda i, n: seen.append(i))
+    assert seen == list(range(1, steps + 1))
+    draw = noise_stream(10)
+    x = x0[0].copy()
+    for i in range(steps):
+        v = dit.step(x[None], gall[i][None])[0]
+        x = port.pingpong(x, v, draw(x.size).reshape(x.shape), sched[i], sched[i + 1])
+    assert np.array_equal(got.view(np.uint32), x.view(np.uint32))
+    dit.free()
+
+
+def test_dit_create_rejects(hip):
+    """unsupported shapes return NULL with an error (the caller falls back to the CPU DiT)."""
+    from aria_amd import HipError
+    from aria_amd.dit import Dit
+    M = model(81)
+    with pytest.raises(HipError):
+        Dit(M, 2, 128, 4, 256, 16, 3, 32)     # head_dim 32
+
+
+def test_dit_config5_step(hip, port, R):
+    """Config 5 shape: 24 q4 blocks (config-4 block, tanh-GELU 4x FFN), T = 1296, batch 2,
+    latent [2, 64, 1296], context [2, 256, 1024]; one teacher-forced step of the 8 (the CPU side
+    costs ~48 block forwards per step), through the graph-captured batched step."""
+    from aria_amd.dit import Dit, random_dit, FFN_GELU
+    depth, ed, H, inner, C, T, Sc, rot = 24, 1024, 16, 4096, 64, 1296, 256, 32
+    M = random_dit(rng(0xC5), depth, ed, inner, C, 0, ffn=FFN_GELU)
+    c, s = R.rope_freqs(T, rot, 10000.0)
+    x, ced, g = inputs(0xC50, 2, C, T, Sc, ed)
+    dit = Dit(M, depth, ed, H, inner, C, 0, rot, precision=4, ffn=FFN_GELU)
+    dit.set_request(T, [ced[0], ced[1]], c, s)
+    dit.step(x, g)                       # captures
+    got = dit.step(x, g)                 # replays
+    assert dit.graph_active
+    for b in range(2):
+        want = ref_step(R, port, M, 4, x[b], ced[b], g[b], c, s, rot, H, ffn=FFN_GELU)
+        d = np.abs(got[b] - want)
+        print(f"config-5 step seq {b}: max|d| {d.max():.3e} max|ref| {np.abs(want).max():.3f}", flush=True)
+        assert_close(got[b], want, ATOL, RTOL, f"config-5 step seq {b}")
+    dit.free()
