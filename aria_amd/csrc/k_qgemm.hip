@@ -21,24 +21,30 @@
  * the reference's fp32 dequantized GEMM: activation (and Q4 weight) rounding to fp16,
  * ~2^-11 relative per product, a few 1e-4 of max|y|.
  *
- * Tiling: 256 threads = 4 waves in a 2x2 grid; each wave owns TMW x TNW tiles of 32x32
- * computed with v_mfma_f32_32x32x16_f16 (two MFMAs per 32-wide K slice). Workgroup tile
- * BM = 64*TMW by BN = 64*TNW, picked per shape so the grid fills the 256 CUs evenly.
+ * Tiling: 256 threads = 4 waves in a WGM x WGN grid; each wave owns FM x FN blocks of
+ * 32x32 computed with v_mfma_f32_32x32x16_f16 as W x^T (two MFMAs per 32-wide K slice),
+ * so a lane's accumulators hold 4 consecutive n of one m. Workgroup tiles run from
+ * 64x64 to 192x128 / 128x256 (m x n), picked per shape (pick_tiles).
  * Pipeline: a ring of three register stages holds raw (still packed) slices; the
  * global loads of slice k+3 are issued while slice k is multiplied out of LDS, so each
  * load has two slice-times to land; a slice is unpacked to fp16 only when it is stored
- * to the LDS double buffer (one barrier per slice).
+ * to the LDS double buffer (one barrier per slice). Loads past the M / N edge re-read the
+ * last row, so the steady-state loop has no branches around its loads.
+ * Epilogue: each wave stages 32 x 32*FN fp32 results at a time through LDS and writes
+ * whole row segments (16 B per lane, coalesced), applying the Q8 scale, bias and GELU.
  * Operand layout of the 32x32x16 MFMA: lane l supplies row (l % 32) and the 8
  * consecutive k at 8*(l / 32); accumulator register r of lane l holds row
  * 8*(r/4) + 4*(l/32) + r%4, column l % 32.
  *
- * Shapes with K % 32 != 0 or unaligned operands take a SIMT fp32 kernel with the same
- * dequant values (k_qgemm_simt).
+ * Shapes with K % 32 != 0, N % 4 != 0 or unaligned operands take a SIMT fp32 kernel with
+ * the same dequant values (k_qgemm_simt).
  */
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 struct QArgs {
@@ -53,109 +59,148 @@ struct QArgs {
     int gelu;   /* epilogue: y = gelu_tanh(acc*scale + b) (the config FFN's activation) */
 };
 
-#define BK 32
-#define LDS_STRIDE (BK + 8)   /* halves per LDS row: 80 B, conflict-free 16 B fragment reads */
+#define BK 32          /* k per slice */
+#define LDS_STRIDE 32  /* halves per LDS row: 64 B, 4 chunks of 8 k */
 
+/* LDS tiles are unpadded [rows][32] halves; chunk c of row r sits at position
+ * c ^ ((r >> 2) & 3). The producers write one 16 B chunk per lane, four lanes per row
+ * (the order that keeps their global loads coalesced), and the MFMA fragment reads take
+ * 32 rows x 2 chunks per instruction: with this swizzle neither pattern has bank
+ * conflicts on gfx950 (64 banks, 16 lanes per cycle for 16 B accesses). */
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * LDS_STRIDE + ((chunk ^ ((row >> 2) & 3)) << 3); }
+/* producer slot c -> (row, chunk), row-major */
+__device__ __forceinline__ int slot_row(int c) { return c >> 2; }
+__device__ __forceinline__ int slot_chunk(int c) { return c & 3; }
+
+/* two fp32 -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32) */
 __device__ __forceinline__ uint32_t pack2h(float a, float b) {
-    return (uint32_t)f2h_bits(a) | ((uint32_t)f2h_bits(b) << 16);
+    const float2_t f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));
 }
 
-/* raw register words per 16-element chunk */
-template <bool AF16> struct RawA { static constexpr int W = AF16 ? 8 : 16; };
-template <int WT> struct RawB { static constexpr int W = (WT == ARIA_WQ8 || WT == ARIA_WQ4) ? 4 : 8; };
-
-/* ---- global -> raw registers (no arithmetic, so the loads stay in flight) ---- */
-template <bool AF16>
-__device__ __forceinline__ void ld_a(uint32_t *r, const QArgs &a, int m, int k) {
-    constexpr int W = RawA<AF16>::W;
-    if (m >= a.M) {
-#pragma unroll
-        for (int i = 0; i < W; i++) r[i] = 0u;
-        return;
-    }
-    const uint4 *p = AF16 ? reinterpret_cast<const uint4 *>((const uint16_t *)a.x + (size_t)m * a.K + k)
-                          : reinterpret_cast<const uint4 *>((const float *)a.x + (size_t)m * a.K + k);
-#pragma unroll
-    for (int j = 0; j < W / 4; j++) {
-        const uint4 u = p[j];
-        r[4 * j] = u.x; r[4 * j + 1] = u.y; r[4 * j + 2] = u.z; r[4 * j + 3] = u.w;
-    }
+/* Q8: four int8 in one word -> two words of fp16 pairs, exactly. Each byte is biased to
+ * unsigned (b ^ 0x80 = b + 128) and placed under the fp16 exponent of 1024
+ * (0x64XX = 1024 + XX), then 1152 is subtracted: an exact integer in [-127, 127]. */
+__device__ __forceinline__ void q8x4_to_h(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
 }
 
-template <int WT>
-__device__ __forceinline__ void ld_b(uint32_t *r, const QArgs &a, int n, int k) {
-    constexpr int W = RawB<WT>::W;
-    if (n >= a.N) {
-#pragma unroll
-        for (int i = 0; i < W; i++) r[i] = 0u;
-        return;
-    }
-    if (WT == ARIA_WQ8) {
-        const uint4 u = *reinterpret_cast<const uint4 *>((const int8_t *)a.q + (size_t)n * a.K + k);
-        r[0] = u.x; r[1] = u.y; r[2] = u.z; r[3] = u.w;
-    } else if (WT == ARIA_WQ4) {
-        const uint2 u = *reinterpret_cast<const uint2 *>((const uint8_t *)a.q + (size_t)n * (a.K >> 1) + (k >> 1));
-        const uint2 pr = *reinterpret_cast<const uint2 *>(a.scale + ((size_t)n * a.nblk + (k >> 5)) * 2);
-        r[0] = u.x; r[1] = u.y; r[2] = pr.x; r[3] = pr.y;
-    } else {
-        const uint4 *p = reinterpret_cast<const uint4 *>((const uint16_t *)a.q + (size_t)n * a.K + k);
-        const uint4 u0 = p[0], u1 = p[1];
-        r[0] = u0.x; r[1] = u0.y; r[2] = u0.z; r[3] = u0.w;
-        r[4] = u1.x; r[5] = u1.y; r[6] = u1.z; r[7] = u1.w;
-    }
-}
+/* ---- tile configuration: a 2-D grid of WGM x WGN waves, each owning FM x FN 32x32
+ * blocks (FM along the activation rows m, FN along the weight rows n) ---- */
+template <int FM_, int FN_, int WGM_, int WGN_>
+struct Cfg {
+    static constexpr int FM = FM_, FN = FN_, WGM = WGM_, WGN = WGN_;
+    static constexpr int BM = 32 * FM * WGM, BN = 32 * FN * WGN, NT = 64 * WGM * WGN;
+    /* epilogue staging: per wave 32 rows x 32*FN fp32, rows padded by 16 B */
+    static constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
+    static constexpr int TILE_BYTES = 2 * (BM + BN) * LDS_STRIDE * 2, EPI_BYTES = 4 * 32 * EPI_STRIDE;
+    static constexpr int LDS_BYTES = TILE_BYTES > EPI_BYTES ? TILE_BYTES : EPI_BYTES;
+};
 
-/* ---- raw registers -> 16 halves in LDS ---- */
-__device__ __forceinline__ void st_lds8(uint16_t *dst, const uint32_t (&o)[8]) {
-    uint4 *d = reinterpret_cast<uint4 *>(dst);
-    d[0] = make_uint4(o[0], o[1], o[2], o[3]);
-    d[1] = make_uint4(o[4], o[5], o[6], o[7]);
-}
+/* per-thread staging of one BK slice in its global encoding; every chunk is 8 k of one
+ * row: activations 16 B fp16 or 32 B fp32, weights 8 B int8 (Q8), 4 B nibbles + the
+ * block's [min, step] (Q4), 16 B fp16 */
+template <class C, int WT, bool AF16>
+struct Stage {
+    static constexpr int CH = C::BM * (BK / 8), XI = (CH + C::NT - 1) / C::NT, XW = AF16 ? 4 : 8;
+    static constexpr int WCH = C::BN * (BK / 8), WI = (WCH + C::NT - 1) / C::NT;
+    static constexpr int WW = (WT == ARIA_WQ8) ? 2 : (WT == ARIA_WQ4) ? 3 : 4;
+    static_assert(C::BM % 32 == 0 && C::BN % 32 == 0, "tiles are whole MFMA blocks");
+    uint32_t x[XI][XW];
+    uint32_t w[WI][WW];
+};
 
-template <bool AF16>
-__device__ __forceinline__ void cv_a(uint16_t *dst, const uint32_t *r) {
-    uint32_t o[8];
-    if (AF16) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) o[i] = r[i];
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            o[i] = pack2h(__builtin_bit_cast(float, r[2 * i]), __builtin_bit_cast(float, r[2 * i + 1]));
-    }
-    st_lds8(dst, o);
-}
+template <class C, int WT, bool AF16>
+struct Tile {
+    using S = Stage<C, WT, AF16>;
+    const QArgs &q;
+    int tid, m0, n0;
+    uint16_t *Xs, *Ws;   /* [2][rows * LDS_STRIDE] */
 
-template <int WT>
-__device__ __forceinline__ void cv_b(uint16_t *dst, const uint32_t *r) {
-    uint32_t o[8];
-    if (WT == ARIA_WQ8) {
+    /* rows past the edge re-read the last row: their products land only in output rows
+     * or columns the epilogue never stores, and the branch-free loads keep the vmcnt
+     * accounting exact so the prefetch stays in flight */
+    __device__ __forceinline__ void load(S &s, int kt) const {
+        const int k0 = kt * BK;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t w = r[j];
-            const int b0 = (int)(int8_t)(w & 0xFF), b1 = (int)(int8_t)((w >> 8) & 0xFF);
-            const int b2 = (int)(int8_t)((w >> 16) & 0xFF), b3 = (int)(int8_t)(w >> 24);
-            o[2 * j] = pack2h((float)b0, (float)b1);
-            o[2 * j + 1] = pack2h((float)b2, (float)b3);
-        }
-    } else if (WT == ARIA_WQ4) {
-        const float mn = __builtin_bit_cast(float, r[2]), st = __builtin_bit_cast(float, r[3]);
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t byte = (r[j] >> (8 * e)) & 0xFF;
-                const float lo = mn + (float)(byte & 0xF) * st;   /* even k: low nibble */
-                const float hi = mn + (float)(byte >> 4) * st;    /* odd k: high nibble */
-                o[4 * j + e] = pack2h(lo, hi);
+        for (int i = 0; i < S::XI; i++) {
+            const int c = tid + i * C::NT;
+            if (S::CH % C::NT != 0 && c >= S::CH) break;
+            const int m = min(m0 + slot_row(c), q.M - 1), k = k0 + 8 * slot_chunk(c);
+            if (AF16) {
+                const uint4 u = *reinterpret_cast<const uint4 *>((const uint16_t *)q.x + (size_t)m * q.K + k);
+                s.x[i][0] = u.x; s.x[i][1] = u.y; s.x[i][2] = u.z; s.x[i][3] = u.w;
+            } else {
+                const uint4 *p = reinterpret_cast<const uint4 *>((const float *)q.x + (size_t)m * q.K + k);
+                const uint4 u0 = p[0], u1 = p[1];
+                s.x[i][0] = u0.x; s.x[i][1] = u0.y; s.x[i][2] = u0.z; s.x[i][3] = u0.w;
+                s.x[i][4] = u1.x; s.x[i][5] = u1.y; s.x[i][6] = u1.z; s.x[i][7] = u1.w;
             }
         }
-    } else {
 #pragma unroll
-        for (int i = 0; i < 8; i++) o[i] = r[i];
+        for (int i = 0; i < S::WI; i++) {
+            const int c = tid + i * C::NT;
+            if (S::WCH % C::NT != 0 && c >= S::WCH) break;
+            const int n = min(n0 + slot_row(c), q.N - 1), k = k0 + 8 * slot_chunk(c);
+            if (WT == ARIA_WQ8) {
+                const uint2 u = *reinterpret_cast<const uint2 *>((const int8_t *)q.q + (size_t)n * q.K + k);
+                s.w[i][0] = u.x; s.w[i][1] = u.y;
+            } else if (WT == ARIA_WQ4) {
+                s.w[i][0] = *reinterpret_cast<const uint32_t *>((const uint8_t *)q.q + (size_t)n * (q.K >> 1) + (k >> 1));
+                const uint2 pr = *reinterpret_cast<const uint2 *>(q.scale + ((size_t)n * q.nblk + (k >> 5)) * 2);
+                s.w[i][1] = pr.x; s.w[i][2] = pr.y;
+            } else {
+                const uint4 u = *reinterpret_cast<const uint4 *>((const uint16_t *)q.q + (size_t)n * q.K + k);
+                s.w[i][0] = u.x; s.w[i][1] = u.y; s.w[i][2] = u.z; s.w[i][3] = u.w;
+            }
+        }
     }
-    st_lds8(dst, o);
-}
+
+    /* unpack to fp16 and write the slice into LDS buffer buf */
+    __device__ __forceinline__ void store(const S &s, int buf) const {
+        uint16_t *X = Xs + buf * (C::BM * LDS_STRIDE), *W = Ws + buf * (C::BN * LDS_STRIDE);
+#pragma unroll
+        for (int i = 0; i < S::XI; i++) {
+            const int c = tid + i * C::NT;
+            if (S::CH % C::NT != 0 && c >= S::CH) break;
+            uint4 o;
+            if (AF16) {
+                o = make_uint4(s.x[i][0], s.x[i][1], s.x[i][2], s.x[i][3]);
+            } else {
+                const float *f = reinterpret_cast<const float *>(s.x[i]);
+                o = make_uint4(pack2h(f[0], f[1]), pack2h(f[2], f[3]), pack2h(f[4], f[5]), pack2h(f[6], f[7]));
+            }
+            *reinterpret_cast<uint4 *>(&X[lds_off(slot_row(c), slot_chunk(c))]) = o;
+        }
+#pragma unroll
+        for (int i = 0; i < S::WI; i++) {
+            const int c = tid + i * C::NT;
+            if (S::WCH % C::NT != 0 && c >= S::WCH) break;
+            uint4 o;
+            if (WT == ARIA_WQ8) {
+                q8x4_to_h(s.w[i][0], o.x, o.y);
+                q8x4_to_h(s.w[i][1], o.z, o.w);
+            } else if (WT == ARIA_WQ4) {
+                /* w = min + nib * step in fp32 (the reference's dequant value), rounded to
+                 * fp16; even k in the low nibble */
+                const float mn = __builtin_bit_cast(float, s.w[i][1]), st = __builtin_bit_cast(float, s.w[i][2]);
+                const uint32_t lo = s.w[i][0] & 0x0F0F0F0Fu, hi = (s.w[i][0] >> 4) & 0x0F0F0F0Fu;
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    h[e] = pack2h(__builtin_fmaf((float)((lo >> (8 * e)) & 0xFF), st, mn),
+                                  __builtin_fmaf((float)((hi >> (8 * e)) & 0xFF), st, mn));
+                o = make_uint4(h[0], h[1], h[2], h[3]);
+            } else {
+                o = make_uint4(s.w[i][0], s.w[i][1], s.w[i][2], s.w[i][3]);
+            }
+            *reinterpret_cast<uint4 *>(&W[lds_off(slot_row(c), slot_chunk(c))]) = o;
+        }
+    }
+};
 
 /* Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
  * workgroup g runs on XCD g % 8. Tile t = (g % 8) * ceil(T/8) + g / 8 gives each
@@ -166,106 +211,79 @@ __device__ __forceinline__ int xcd_tile(int g, int T) {
     return (g & 7) * per + (g >> 3);
 }
 
-template <int WT, bool AF16, int TMW, int TNW>
-struct QTile {
-    static constexpr int BM = 64 * TMW, BN = 64 * TNW;
-    static constexpr int ACH = BM * 2, BCH = BN * 2;   /* 16-element chunks per 32-wide slice */
-    static constexpr int AIT = (ACH + 255) / 256, BIT = (BCH + 255) / 256;
-    static constexpr int WA = RawA<AF16>::W, WB = RawB<WT>::W;
-    struct Stage {
-        uint32_t a[AIT][WA];
-        uint32_t b[BIT][WB];
-    };
-
-    const QArgs &q;
-    int tid, m0, n0;
-    uint16_t *As, *Bs;   /* [2][rows * LDS_STRIDE] */
-
-    __device__ __forceinline__ void load(Stage &s, int kt) const {
-        const int k0 = kt * BK;
-#pragma unroll
-        for (int i = 0; i < AIT; i++) {
-            const int c = tid + i * 256;
-            if (c < ACH) ld_a<AF16>(s.a[i], q, m0 + (c >> 1), k0 + 16 * (c & 1));
-        }
-#pragma unroll
-        for (int i = 0; i < BIT; i++) {
-            const int c = tid + i * 256;
-            if (c < BCH) ld_b<WT>(s.b[i], q, n0 + (c >> 1), k0 + 16 * (c & 1));
-        }
-    }
-    __device__ __forceinline__ void store(const Stage &s, int buf) const {
-        uint16_t *A = As + buf * (BM * LDS_STRIDE), *B = Bs + buf * (BN * LDS_STRIDE);
-#pragma unroll
-        for (int i = 0; i < AIT; i++) {
-            const int c = tid + i * 256;
-            if (c < ACH) cv_a<AF16>(&A[(c >> 1) * LDS_STRIDE + 16 * (c & 1)], s.a[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < BIT; i++) {
-            const int c = tid + i * 256;
-            if (c < BCH) cv_b<WT>(&B[(c >> 1) * LDS_STRIDE + 16 * (c & 1)], s.b[i]);
-        }
-    }
-};
-
-template <int WT, bool AF16, int TMW, int TNW>
-__global__ __launch_bounds__(256) void k_qgemm_mfma(QArgs a, int NT, int T) {
-    using Q = QTile<WT, AF16, TMW, TNW>;
-    constexpr int BM = Q::BM, BN = Q::BN;
-    __shared__ __attribute__((aligned(16))) uint16_t As[2 * BM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2 * BN * LDS_STRIDE];
+template <class C, int WT, bool AF16>
+__global__ __launch_bounds__(C::NT) void k_qgemm_mfma(QArgs a, int NTN, int T) {
+    using TL = Tile<C, WT, AF16>;
+    using S = typename TL::S;
+    constexpr int FM = C::FM, FN = C::FN, BM = C::BM, BN = C::BN;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[C::LDS_BYTES / 2];
+    uint16_t *Xs = lds, *Ws = lds + 2 * BM * LDS_STRIDE;
 
     const int t = xcd_tile(blockIdx.x, T);
     if (t >= T) return;                     /* uniform per workgroup */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const Q qt{a, tid, (t / NT) * BM, (t % NT) * BN, As, Bs};
+    const int wm = wave / C::WGN, wn = wave % C::WGN;
+    const TL tl{a, tid, (t / NTN) * BM, (t % NTN) * BN, Xs, Ws};
     const int KT = a.K / BK;
 
-    f32x16_t acc[TMW][TNW];
+    /* acc[i][j]: the 32x32 block (weight rows j, activation rows i), computed as
+     * W x^T so a lane holds 4 consecutive n of one m */
+    f32x16_t acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < TMW; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < TNW; j++)
+        for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    const int lrow = lane & 31, lk = 8 * (lane >> 5);
+    const int lrow = lane & 31, lh = lane >> 5;
     auto compute = [&](int buf) {
-        const uint16_t *A = As + buf * (BM * LDS_STRIDE), *B = Bs + buf * (BN * LDS_STRIDE);
+        const uint16_t *X = Xs + buf * (BM * LDS_STRIDE), *W = Ws + buf * (BN * LDS_STRIDE);
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
-            half8_t af[TMW], bf[TNW];
+            half8_t xf[FM], wf[FN];
 #pragma unroll
-            for (int i = 0; i < TMW; i++)
-                af[i] = *reinterpret_cast<const half8_t *>(&A[(wm * 32 * TMW + i * 32 + lrow) * LDS_STRIDE + ks * 16 + lk]);
+            for (int j = 0; j < FN; j++)
+                wf[j] = *reinterpret_cast<const half8_t *>(&W[lds_off(wn * 32 * FN + j * 32 + lrow, 2 * ks + lh)]);
 #pragma unroll
-            for (int j = 0; j < TNW; j++)
-                bf[j] = *reinterpret_cast<const half8_t *>(&B[(wn * 32 * TNW + j * 32 + lrow) * LDS_STRIDE + ks * 16 + lk]);
+            for (int i = 0; i < FM; i++)
+                xf[i] = *reinterpret_cast<const half8_t *>(&X[lds_off(wm * 32 * FM + i * 32 + lrow, 2 * ks + lh)]);
 #pragma unroll
-            for (int i = 0; i < TMW; i++)
+            for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < TNW; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[i][j], 0, 0, 0);
         }
     };
 
-    /* ring of three raw stages: at slice kt, stage (kt+1)%3 holds slice kt+1 and
-     * stage kt%3 receives slice kt+3 */
-    typename Q::Stage s0, s1, s2;
-    qt.load(s0, 0);
-    if (KT > 1) qt.load(s1, 1);
-    if (KT > 2) qt.load(s2, 2);
-    qt.store(s0, 0);
+    /* ring of three register stages: at slice kt, stage (kt+1)%3 holds slice kt+1 and
+     * stage kt%3 receives slice kt+3. Steady-state steps store and load unconditionally
+     * (no path without the loads, so the compiler's vmcnt waits stay exact); the last
+     * few steps run the guarded form. */
+    S s0, s1, s2;
+    tl.load(s0, 0);
+    if (KT > 1) tl.load(s1, 1);
+    if (KT > 2) tl.load(s2, 2);
+    tl.store(s0, 0);
     __syncthreads();
-    auto step = [&](int kt, typename Q::Stage &nxt, typename Q::Stage &fill) {
+    auto full = [&](int kt, S &nxt, S &fill) {
         compute(kt & 1);
-        if (kt + 1 < KT) qt.store(nxt, (kt + 1) & 1);
-        if (kt + 3 < KT) qt.load(fill, kt + 3);
+        tl.store(nxt, (kt + 1) & 1);
+        tl.load(fill, kt + 3);
+        __syncthreads();
+    };
+    auto step = [&](int kt, S &nxt, S &fill) {
+        compute(kt & 1);
+        if (kt + 1 < KT) tl.store(nxt, (kt + 1) & 1);
+        if (kt + 3 < KT) tl.load(fill, kt + 3);
         __syncthreads();
     };
     int kt = 0;
+    for (; kt + 6 <= KT; kt += 3) {
+        full(kt, s1, s0);
+        full(kt + 1, s2, s1);
+        full(kt + 2, s0, s2);
+    }
     for (; kt + 3 <= KT; kt += 3) {
         step(kt, s1, s0);
         step(kt + 1, s2, s1);
@@ -274,27 +292,53 @@ __global__ __launch_bounds__(256) void k_qgemm_mfma(QArgs a, int NT, int T) {
     if (kt < KT) step(kt, s1, s0);
     if (kt + 1 < KT) step(kt + 1, s2, s1);
 
-    /* epilogue: acc register r of lane l -> row 8*(r/4) + 4*(l/32) + r%4, column l%32 */
+    /* epilogue: each wave stages 32 rows of its tile at a time through LDS (fp32, rows
+     * padded), then writes whole row segments: 16 lanes x 16 B per row, coalesced.
+     * acc register r of lane l -> n = 8*(r/4) + 4*(l/32) + r%4, m = l%32 in its block.
+     * The last slice's barrier has released the tile buffers. */
+    float *E = reinterpret_cast<float *>(lds) + wave * (32 * C::EPI_STRIDE / 4);
+    constexpr int CW = 32 * FN;                 /* columns per wave */
+    constexpr int LPR = CW / 4;                 /* lanes per row (16 B each) */
+    constexpr int RPI = 64 / LPR;               /* rows per store instruction */
+    const int ecol = (lane % LPR) * 4, erow = lane / LPR;
+    const int nb = tl.n0 + wn * CW + ecol;      /* this lane's 4 output columns */
+    float4 sc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), bb = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (nb < a.N) {
+        if (WT == ARIA_WQ8) sc = *reinterpret_cast<const float4 *>(a.scale + nb);
+        if (a.bias) bb = *reinterpret_cast<const float4 *>(a.bias + nb);
+    }
 #pragma unroll
-    for (int j = 0; j < TNW; j++) {
-        const int n = qt.n0 + wn * 32 * TNW + j * 32 + (lane & 31);
-        if (n >= a.N) continue;
-        const float sc = (WT == ARIA_WQ8) ? a.scale[n] : 1.0f;
-        const float bb = a.bias ? a.bias[n] : 0.0f;
+    for (int i = 0; i < FM; i++) {
 #pragma unroll
-        for (int i = 0; i < TMW; i++) {
+        for (int j = 0; j < FN; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = qt.m0 + wm * 32 * TMW + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m >= a.M) continue;
-                float v = acc[i][j][r];
-                if (WT == ARIA_WQ8) v = v * sc;
-                if (a.bias) v = v + bb;
-                if (a.gelu) v = gelu_tanh_f(v);
-                if (a.y_f16) ((uint16_t *)a.y)[(size_t)m * a.N + n] = f2h_bits(v);
-                else ((float *)a.y)[(size_t)m * a.N + n] = v;
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<float4 *>(reinterpret_cast<char *>(E) + lrow * C::EPI_STRIDE +
+                                            (j * 32 + 8 * g + 4 * lh) * 4) =
+                    make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int it = 0; it < 32 / RPI; it++) {
+            const int r = it * RPI + erow;
+            const int m = tl.m0 + wm * 32 * FM + i * 32 + r;
+            const float4 v4 = *reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(E) +
+                                                                r * C::EPI_STRIDE + ecol * 4);
+            if (m >= a.M || nb >= a.N) continue;
+            float v[4] = {v4.x, v4.y, v4.z, v4.w};
+            const float scv[4] = {sc.x, sc.y, sc.z, sc.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (WT == ARIA_WQ8) v[e] = v[e] * scv[e];
+                if (a.bias) v[e] = v[e] + bv[e];
+                if (a.gelu) v[e] = gelu_tanh_f(v[e]);
             }
+            if (a.y_f16)
+                *reinterpret_cast<uint2 *>((uint16_t *)a.y + (size_t)m * a.N + nb) =
+                    make_uint2(pack2h(v[0], v[1]), pack2h(v[2], v[3]));
+            else
+                *reinterpret_cast<float4 *>((float *)a.y + (size_t)m * a.N + nb) = make_float4(v[0], v[1], v[2], v[3]);
         }
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -359,28 +403,37 @@ __global__ __launch_bounds__(256) void k_qgemm_simt(QArgs a) {
     }
 }
 
-template <int WT, bool AF16, int TMW, int TNW>
-static void launch_tiles(const QArgs &a, hipStream_t s) {
-    constexpr int BM = 64 * TMW, BN = 64 * TNW;
-    const int MT = (a.M + BM - 1) / BM, NT = (a.N + BN - 1) / BN, T = MT * NT;
+template <class C, int WT, bool AF16>
+static void launch_cfg(const QArgs &a, hipStream_t s) {
+    const int MT = (a.M + C::BM - 1) / C::BM, NTN = (a.N + C::BN - 1) / C::BN, T = MT * NTN;
     const int grid = ((T + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_qgemm_mfma<WT, AF16, TMW, TNW>), dim3(grid), dim3(256), 0, s, a, NT, T);
+    hipLaunchKernelGGL((k_qgemm_mfma<C, WT, AF16>), dim3(grid), dim3(C::NT), 0, s, a, NTN, T);
 }
 
-/* Tile shape: estimated time ~ rounds * per-CU tile work / tile efficiency, where a CU
- * runs `occ` workgroups at once and rounds = ceil(T / (256 * occ)). */
+/* workgroup tiles (activation rows x weight rows), index = the `tiles` argument - 1 */
+using C1 = Cfg<3, 2, 2, 2>;   /* 192 x 128 */
+using C2 = Cfg<2, 2, 2, 2>;   /* 128 x 128 */
+using C3 = Cfg<3, 2, 1, 4>;   /*  96 x 256 */
+using C4 = Cfg<3, 1, 1, 4>;   /*  96 x 128 */
+using C5 = Cfg<2, 4, 2, 2>;   /* 128 x 256 */
+using C6 = Cfg<1, 2, 2, 2>;   /*  64 x 128 */
+using C7 = Cfg<2, 1, 2, 2>;   /* 128 x  64 */
+using C8 = Cfg<1, 1, 2, 2>;   /*  64 x  64 */
+#define NCFG 8
+static const int cfg_bm[NCFG] = {192, 128, 96, 96, 128, 64, 128, 64};
+static const int cfg_bn[NCFG] = {128, 128, 256, 128, 256, 128, 64, 64};
+
+/* Tile shape from the shape: a CU holds several workgroups at once, so the busiest CU
+ * carries ceil(tiles / 256) tiles; cost = that count x the tile's MFMA work / the tile's
+ * measured efficiency (bigger wave tiles read less LDS per MFMA; the 128x256 tile runs
+ * one wave per SIMD). */
 static int pick_tiles(int M, int N) {
-    static const int cfg[4][3] = {{2, 2, 3}, {2, 1, 4}, {1, 2, 4}, {1, 1, 6}};   /* TMW, TNW, occ */
-    static const double eff[4] = {1.0, 0.85, 0.85, 0.6};
-    double best = 1e30;
-    int bi = 0;
-    for (int i = 0; i < 4; i++) {
-        const int BM = 64 * cfg[i][0], BN = 64 * cfg[i][1];
-        const long T = (long)((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-        const long slots = 256L * cfg[i][2];
-        const long rounds = (T + slots - 1) / slots;
-        const double load = (double)rounds * cfg[i][2] * (BM / 64) * (BN / 64);
-        const double cost = load / eff[i];
+    static const double eff[NCFG] = {1.0, 0.95, 0.9, 0.85, 0.8, 0.8, 0.8, 0.75};
+    double best = 1e300;
+    int bi = 1;
+    for (int i = 0; i < NCFG; i++) {
+        const long T = (long)((M + cfg_bm[i] - 1) / cfg_bm[i]) * ((N + cfg_bn[i] - 1) / cfg_bn[i]);
+        const double cost = (double)((T + 255) / 256) * cfg_bm[i] * cfg_bn[i] / eff[i];
         if (cost < best - 1e-9) { best = cost; bi = i; }
     }
     return bi;
@@ -388,21 +441,33 @@ static int pick_tiles(int M, int N) {
 
 template <int WT, bool AF16>
 static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
-    const bool aligned = a.K % BK == 0 && ((uintptr_t)a.x & 15u) == 0 && ((uintptr_t)a.q & 15u) == 0 &&
+    const bool aligned = a.K % BK == 0 && a.N % 4 == 0 && ((uintptr_t)a.x & 15u) == 0 &&
+                         ((uintptr_t)a.q & 15u) == 0 && ((uintptr_t)a.y & 15u) == 0 &&
+                         (a.bias == nullptr || ((uintptr_t)a.bias & 15u) == 0) &&
+                         (WT != ARIA_WQ8 || ((uintptr_t)a.scale & 15u) == 0) &&
                          (WT != ARIA_WQ4 || ((uintptr_t)a.scale & 7u) == 0);
     if (!aligned) {
         dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
         hipLaunchKernelGGL((k_qgemm_simt<WT, AF16>), grid, dim3(256), 0, s, a);
         return hipGetLastError();
     }
-    const int c = (tiles >= 1 && tiles <= 4) ? tiles - 1 : pick_tiles(a.M, a.N);
+    if constexpr (!AF16) {   /* fp32 activations: the fallback when no fp16 staging buffer was available */
+        launch_cfg<C2, WT, AF16>(a, s);
+        return hipGetLastError();
+    } else {
+    const int c = (tiles >= 1 && tiles <= NCFG) ? tiles - 1 : pick_tiles(a.M, a.N);
     switch (c) {
-        case 0: launch_tiles<WT, AF16, 2, 2>(a, s); break;
-        case 1: launch_tiles<WT, AF16, 2, 1>(a, s); break;
-        case 2: launch_tiles<WT, AF16, 1, 2>(a, s); break;
-        default: launch_tiles<WT, AF16, 1, 1>(a, s); break;
+        case 0: launch_cfg<C1, WT, AF16>(a, s); break;
+        case 1: launch_cfg<C2, WT, AF16>(a, s); break;
+        case 2: launch_cfg<C3, WT, AF16>(a, s); break;
+        case 3: launch_cfg<C4, WT, AF16>(a, s); break;
+        case 4: launch_cfg<C5, WT, AF16>(a, s); break;
+        case 5: launch_cfg<C6, WT, AF16>(a, s); break;
+        case 6: launch_cfg<C7, WT, AF16>(a, s); break;
+        default: launch_cfg<C8, WT, AF16>(a, s); break;
     }
     return hipGetLastError();
+    }
 }
 
 extern "C" hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,

@@ -135,8 +135,10 @@ int aria_hip_q4_dequant_dev(float *dW, const uint8_t *dq, const float *dscale, i
  * x_f16 / y_f16 select IEEE-half activations / outputs instead of fp32. */
 int aria_hip_qlinear_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
                          const float *dscale, const float *db, int M, int K, int N, void *stream);
-/* As aria_hip_qlinear_dev with an explicit workgroup tile (M x N): 1 = 128x128,
- * 2 = 128x64, 3 = 64x128, 4 = 64x64, 0 = chosen from the shape (tuning knob). */
+/* As aria_hip_qlinear_dev with an explicit workgroup tile (M x N): 1 = 192x128,
+ * 2 = 128x128, 3 = 96x256, 4 = 96x128, 5 = 128x256, 6 = 64x128, 7 = 128x64, 8 = 64x64,
+ * 0 = chosen from the shape (tuning knob; fp32 activations without an fp16 staging
+ * buffer always run 128x128). */
 int aria_hip_qlinear_ex_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
                             const float *dscale, const float *db, int M, int K, int N, int tiles,
                             void *stream);
