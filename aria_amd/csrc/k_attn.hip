@@ -20,10 +20,14 @@
  * over keys do not depend on order). Lanes l and l^32 hold the same query, so the
  * softmax statistics need a single xor-32 exchange.
  *
- * Precision: Q, K, V and P are fp16, accumulation fp32, exp via v_exp_f32.
- * Workgroup: 4 waves x 32 queries = 128 queries of one (batch, head); K and V
- * tiles of 64 keys are staged in LDS (V transposed) with register prefetch of
- * the next tile.
+ * Precision: Q, K, V and P are fp16, accumulation fp32, exp via v_exp_f32. The row sum
+ * l is accumulated on the matrix core from the same fp16 P that multiplies V. The
+ * running max is a lazy reference (moved only when a tile exceeds it by 2^8), so the
+ * accumulators are rarely rescaled; O / l does not depend on the reference chosen.
+ * Workgroup: 4 waves x 32 queries = 128 queries of one (batch, head); K and V tiles of
+ * 64 keys are staged key-major in LDS (swizzled, conflict-free) with register prefetch
+ * of the next tile; the V^T operand is read with the gfx950 transpose load
+ * (ds_read_b64_tr_b16).
  */
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
@@ -121,8 +125,7 @@ extern "C" hipError_t aria_k_qkv_prep(const float *src, int ld, int B, int S, in
 /* ------------------------------------------------------------------------- */
 
 #define KT 64                 /* keys per staged tile */
-#define KS_STRIDE (64 + 8)    /* halves: K tile rows [key][d] */
-#define VT_STRIDE (KT + 8)    /* halves: V^T tile rows [d][key] */
+#define RESCALE_SLACK 8.0f    /* log2 units the running max may lag the true max */
 
 struct AttnArgs {
     const uint16_t *q, *k, *v;   /* [B*H, N, 64] fp16 */
@@ -132,11 +135,39 @@ struct AttnArgs {
     int o_f16;
 };
 
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
 __device__ __forceinline__ half8_t ld_h8(const uint16_t *p) { return *reinterpret_cast<const half8_t *>(p); }
 
+/* K and V tiles are key-major [64 keys][64 d] fp16, 128 B rows, unpadded; the 16 B chunk
+ * c (8 d) of key row r sits at position c ^ swizzle(r):
+ *   K: (r >> 1) & 7 -- the fragment reads (32 keys x one chunk, 16 B per lane) and the
+ *      producer writes (8 lanes per row) are bank-conflict free;
+ *   V: ((r >> 1) & 1) << 2 -- the transpose reads below (4 keys x 32 d per 32 lanes,
+ *      8 B per lane) and the producer writes are bank-conflict free. */
+__device__ __forceinline__ int k_off(int key, int chunk) { return key * 64 + ((chunk ^ ((key >> 1) & 7)) << 3); }
+__device__ __forceinline__ int v_off(int key, int d) {
+    return key * 64 + ((((d >> 3) ^ (((key >> 1) & 1) << 2))) << 3) + (d & 7);
+}
+
+/* V^T operand of O^T = V^T P^T for one 16-key MFMA step: lane l (d row l%32 of block
+ * dt, key group g = l/32) needs V[key][d] for keys kb + 4g + {0..3} and kb + 8 + 4g +
+ * {0..3}. ds_read_b64_tr_b16 returns, to lane 4w+c of each 16-lane group, element c of
+ * the 8 B rows addressed by lanes 4v+w (v = 0..3): addressing key kb' + v at d0 + 4w
+ * delivers V[kb'+0..3][d0 + (lane & 15)] to each lane (voff below). */
+
+/* fp32 pair -> packed fp16, round to nearest even */
+__device__ __forceinline__ uint32_t pack2h_rn(float x, float y) {
+    typedef float float2_v __attribute__((ext_vector_type(2)));
+    typedef _Float16 half2_v __attribute__((ext_vector_type(2)));
+    const float2_v f = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_v));
+}
+
 __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * KS_STRIDE];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64 * VT_STRIDE];
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][KT * 64];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
     const int bh = blockIdx.y;
@@ -145,119 +176,147 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
     const uint16_t *Kh = a.k + (size_t)bh * a.Nk * 64;
     const uint16_t *Vh = a.v + (size_t)bh * a.Nk * 64;
 
-    /* Q^T fragments (B operand of S^T = K Q^T): query q0 + l32, d = 16*ds + 8g + [0,8) */
+    /* Q^T fragments (B operand of S^T = K Q^T): query q0 + l32, d = 16*ds + 8g + [0,8);
+     * queries past Nq re-read the last one (their outputs are not stored) */
     half8_t qf[4];
     {
-        const int qi = q0 + l32;
+        const int qi = min(q0 + l32, a.Nq - 1);
 #pragma unroll
-        for (int ds = 0; ds < 4; ds++) {
-            if (qi < a.Nq) qf[ds] = ld_h8(Qh + (size_t)qi * 64 + 16 * ds + 8 * g);
-            else qf[ds] = (half8_t){};
-        }
+        for (int ds = 0; ds < 4; ds++) qf[ds] = ld_h8(Qh + (size_t)qi * 64 + 16 * ds + 8 * g);
     }
 
-    /* tile staging: thread t loads key t/4, d chunk 16*(t%4) of K and V */
-    const int skey = tid >> 2, sd = 16 * (tid & 3);
-    uint32_t rk[8], rv[8];
+    /* tile staging: slots t and t+256 = (key row s>>3, 16 B chunk s&7) of K and V; keys
+     * past Nk re-read the last key (their probabilities are exactly zero) */
+    uint4 rk0, rk1, rv0, rv1;
+    const int sl0 = tid, sl1 = tid + 256;
     auto gload = [&](int kt0) {
-        const int key = kt0 + skey;
-        const bool ok = key < a.Nk;
-        const size_t off = (size_t)(ok ? key : 0) * 64 + sd;   /* always an in-bounds address */
-        const uint4 k0 = *reinterpret_cast<const uint4 *>(Kh + off);
-        const uint4 k1 = *reinterpret_cast<const uint4 *>(Kh + off + 8);
-        const uint4 v0 = *reinterpret_cast<const uint4 *>(Vh + off);
-        const uint4 v1 = *reinterpret_cast<const uint4 *>(Vh + off + 8);
-        rk[0] = ok ? k0.x : 0u; rk[1] = ok ? k0.y : 0u; rk[2] = ok ? k0.z : 0u; rk[3] = ok ? k0.w : 0u;
-        rk[4] = ok ? k1.x : 0u; rk[5] = ok ? k1.y : 0u; rk[6] = ok ? k1.z : 0u; rk[7] = ok ? k1.w : 0u;
-        rv[0] = ok ? v0.x : 0u; rv[1] = ok ? v0.y : 0u; rv[2] = ok ? v0.z : 0u; rv[3] = ok ? v0.w : 0u;
-        rv[4] = ok ? v1.x : 0u; rv[5] = ok ? v1.y : 0u; rv[6] = ok ? v1.z : 0u; rv[7] = ok ? v1.w : 0u;
+        const size_t off0 = (size_t)min(kt0 + (sl0 >> 3), a.Nk - 1) * 64 + 8 * (sl0 & 7);
+        const size_t off1 = (size_t)min(kt0 + (sl1 >> 3), a.Nk - 1) * 64 + 8 * (sl1 & 7);
+        rk0 = *reinterpret_cast<const uint4 *>(Kh + off0);
+        rv0 = *reinterpret_cast<const uint4 *>(Vh + off0);
+        rk1 = *reinterpret_cast<const uint4 *>(Kh + off1);
+        rv1 = *reinterpret_cast<const uint4 *>(Vh + off1);
     };
     auto sstore = [&](int buf) {
-        uint4 *dk = reinterpret_cast<uint4 *>(&Ks[buf][skey * KS_STRIDE + sd]);
-        dk[0] = make_uint4(rk[0], rk[1], rk[2], rk[3]);
-        dk[1] = make_uint4(rk[4], rk[5], rk[6], rk[7]);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            Vt[buf][(sd + 2 * i) * VT_STRIDE + skey] = (uint16_t)(rv[i] & 0xFFFF);
-            Vt[buf][(sd + 2 * i + 1) * VT_STRIDE + skey] = (uint16_t)(rv[i] >> 16);
-        }
+        *reinterpret_cast<uint4 *>(&Ks[buf][k_off(sl0 >> 3, sl0 & 7)]) = rk0;
+        *reinterpret_cast<uint4 *>(&Vs[buf][v_off(sl0 >> 3, 8 * (sl0 & 7))]) = rv0;
+        *reinterpret_cast<uint4 *>(&Ks[buf][k_off(sl1 >> 3, sl1 & 7)]) = rk1;
+        *reinterpret_cast<uint4 *>(&Vs[buf][v_off(sl1 >> 3, 8 * (sl1 & 7))]) = rv1;
     };
 
-    f32x16_t oacc[2];
+    f32x16_t oacc[2], lacc;
 #pragma unroll
-    for (int r = 0; r < 16; r++) { oacc[0][r] = 0.0f; oacc[1][r] = 0.0f; }
-    float m_run = -INFINITY, l_run = 0.0f;
+    for (int r = 0; r < 16; r++) { oacc[0][r] = 0.0f; oacc[1][r] = 0.0f; lacc[r] = 0.0f; }
+    const half8_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
+                          (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+    float m_use = -INFINITY;   /* running reference max, scaled (log2) units */
+
+    /* per-lane LDS offsets (halves) of every fragment read, hoisted out of the key loop */
+    int koff[2][4], voff[4][2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int ds = 0; ds < 4; ds++) koff[kb][ds] = k_off(32 * kb + l32, 2 * ds + g);
+    {
+        const int v = (lane & 15) >> 2, w = lane & 3, G = lane >> 4;
+#pragma unroll
+        for (int s16 = 0; s16 < 4; s16++)
+#pragma unroll
+            for (int dt = 0; dt < 2; dt++) {
+                const int key = 16 * s16 + 4 * (G >> 1) + v, d0 = 32 * dt + 16 * (G & 1) + 4 * w;
+                voff[s16][dt][0] = v_off(key, d0);
+                voff[s16][dt][1] = v_off(key + 8, d0);
+            }
+    }
+
+    /* one 64-key tile from LDS buffer BUF (a compile-time constant, so every LDS offset
+     * is an immediate) */
+    auto tile = [&](const int kt0, const uint16_t *K, const uint16_t *V) {
+        /* S^T [64 keys x 32 queries] as two 32-key blocks */
+        f32x16_t sc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) sc[kb][r] = 0.0f;
+#pragma unroll
+            for (int ds = 0; ds < 4; ds++)
+                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ld_h8(K + koff[kb][ds]), qf[ds], sc[kb], 0, 0, 0);
+        }
+        if (kt0 + KT > a.Nk) {   /* ragged last tile: keys past the end get -inf */
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    if (kt0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3) >= a.Nk) sc[kb][r] = -INFINITY;
+        }
+        /* tile max over this lane's 32 keys and the partner lane's 32 */
+        float m3[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            m3[i] = fmaxf(fmaxf(sc[i >> 2][4 * (i & 3)], sc[i >> 2][4 * (i & 3) + 1]),
+                          fmaxf(sc[i >> 2][4 * (i & 3) + 2], sc[i >> 2][4 * (i & 3) + 3]));
+        float mt = fmaxf(fmaxf(fmaxf(m3[0], m3[1]), fmaxf(m3[2], m3[3])), fmaxf(fmaxf(m3[4], m3[5]), fmaxf(m3[6], m3[7])));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, ARIA_WAVE)) * a.scale_log2;
+        /* lazy rescale: the reference max only moves when the tile max exceeds it by more
+         * than RESCALE_SLACK (probabilities stay <= 2^8, exact in fp16's range); the final
+         * O / l is unchanged by the choice of reference */
+        if (__ballot(mt > m_use + RESCALE_SLACK)) {
+            const float m_new = fmaxf(m_use, mt);
+            const float alpha = __builtin_amdgcn_exp2f(m_use - m_new);
+#pragma unroll
+            for (int r = 0; r < 16; r++) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; lacc[r] *= alpha; }
+            m_use = m_new;
+        }
+        /* P^T = exp2(s * scale - m) in fp16; MFMA step ks of block kb takes accumulator
+         * registers 8ks..8ks+7 (keys 16ks + 4g + {0..3}, 16ks + 8 + 4g + {0..3}) */
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                float pv[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * ks + i], a.scale_log2, -m_use));
+                const half8_t pf = __builtin_bit_cast(half8_t, make_uint4(pack2h_rn(pv[0], pv[1]), pack2h_rn(pv[2], pv[3]),
+                                                                          pack2h_rn(pv[4], pv[5]), pack2h_rn(pv[6], pv[7])));
+                const int s16 = 2 * kb + ks;
+#pragma unroll
+                for (int dt = 0; dt < 2; dt++) {
+                    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[s16][dt][0]));
+                    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[s16][dt][1]));
+                    const half4_t hl = __builtin_bit_cast(half4_t, lo), hh = __builtin_bit_cast(half4_t, hi);
+                    const half8_t vf = {hl[0], hl[1], hl[2], hl[3], hh[0], hh[1], hh[2], hh[3]};
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, oacc[dt], 0, 0, 0);
+                }
+                /* row sums of the rounded P on the matrix core: every row of lacc = sum_k P */
+                lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pf, lacc, 0, 0, 0);
+            }
+        }
+    };
 
     const int ntiles = (a.Nk + KT - 1) / KT;
     gload(0);
     sstore(0);
     __syncthreads();
-    for (int t = 0; t < ntiles; t++) {
-        const int buf = t & 1, kt0 = t * KT;
-        if (t + 1 < ntiles) gload(kt0 + KT);
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-            const int kb = half * 32;   /* key offset inside the tile */
-            /* S^T [32 keys x 32 queries] */
-            f32x16_t s;
-#pragma unroll
-            for (int r = 0; r < 16; r++) s[r] = 0.0f;
-#pragma unroll
-            for (int ds = 0; ds < 4; ds++) {
-                const half8_t kf = ld_h8(&Ks[buf][(kb + l32) * KS_STRIDE + 16 * ds + 8 * g]);
-                s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ds], s, 0, 0, 0);
-            }
-            /* online softmax over this lane's 16 keys + the partner lane's 16 */
-            float mt = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = kt0 + kb + 8 * (r >> 2) + 4 * g + (r & 3);
-                s[r] = key < a.Nk ? s[r] * a.scale_log2 : -INFINITY;
-                mt = fmaxf(mt, s[r]);
-            }
-            mt = fmaxf(mt, __shfl_xor(mt, 32, ARIA_WAVE));
-            const float m_new = fmaxf(m_run, mt);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            float rs = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                s[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
-                rs += s[r];
-            }
-            rs += __shfl_xor(rs, 32, ARIA_WAVE);
-            l_run = l_run * alpha + rs;
-            m_run = m_new;
-#pragma unroll
-            for (int r = 0; r < 16; r++) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
-            /* P^T fragments: MFMA step ks takes accumulator registers 8ks..8ks+7 */
-            half8_t pf[2];
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-                for (int i = 0; i < 8; i++) pf[ks][i] = (_Float16)s[8 * ks + i];
-            /* O^T [64 d x 32 q] += V^T [d x keys] P^T; V^T row d, keys of step ks for lane group g:
-             * kb + 16ks + 4g + {0..3} and kb + 16ks + 8 + 4g + {0..3} */
-#pragma unroll
-            for (int dt = 0; dt < 2; dt++) {
-#pragma unroll
-                for (int ks = 0; ks < 2; ks++) {
-                    const uint16_t *vp = &Vt[buf][(dt * 32 + l32) * VT_STRIDE + kb + 16 * ks + 4 * g];
-                    const half4_t lo = *reinterpret_cast<const half4_t *>(vp);
-                    const half4_t hi = *reinterpret_cast<const half4_t *>(vp + 8);
-                    const half8_t vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[ks], oacc[dt], 0, 0, 0);
-                }
-            }
-        }
-        /* buffer buf^1 was last read in iteration t-1, which ended with a barrier */
-        if (t + 1 < ntiles) sstore(buf ^ 1);
+    /* two tiles per trip so each LDS buffer is a fixed address; buffer b^1 was last read
+     * one tile earlier, before that tile's closing barrier */
+    for (int t = 0; t < ntiles; t += 2) {
+        if (t + 1 < ntiles) gload((t + 1) * KT);
+        tile(t * KT, Ks[0], Vs[0]);
+        if (t + 1 < ntiles) sstore(1);
         __syncthreads();
+        if (t + 1 < ntiles) {
+            if (t + 2 < ntiles) gload((t + 2) * KT);
+            tile((t + 1) * KT, Ks[1], Vs[1]);
+            if (t + 2 < ntiles) sstore(0);
+            __syncthreads();
+        }
     }
 
     /* O[q, d] = O^T[d, q] / l ; lane holds query q0 + l32, d = 32dt + 8(r/4) + 4g + r%4 */
     const int qi = q0 + l32;
     if (qi >= a.Nq) return;
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    const float inv = 1.0f / lacc[0];
     const int b = bh / a.H, h = bh % a.H;
     const size_t orow = ((size_t)b * a.Nq + qi) * (size_t)(a.H * 64) + h * 64;
 #pragma unroll
