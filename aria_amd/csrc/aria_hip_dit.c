@@ -7,16 +7,17 @@
  *
  *   mod      = to_scale_shift_gate + gcond, chunk-major            k_mod_chunks
  *   self:    h16 = rmsnorm(x, pre_norm)*(1+scale)+shift  (fp16)    k_rownorm (fused adaLN)
- *            qkv = h16 . sa_to_qkv^T                                k_qgemm (Q8)
- *            q,k,v heads, q/k rmsnorm + RoPE (fp16, head-major)     k_qkv_prep
+ *            q,k,v = h16 . sa_to_qkv^T, split into heads, q/k rmsnorm + RoPE, fp16
+ *            head-major                                             k_qgemm (Q8, HEADS epilogue)
  *            att = softmax(q k^T / 8) v (fp16, heads merged)        k_flash_attn
- *            x  += (att . sa_to_out^T) * sigmoid(1 - gate)          k_qgemm, k_gate_residual
- *   cross:   h16 = rmsnorm(x, cross_norm); q = h16 . ca_to_q^T; q-norm; attention over the
- *            request's cached K/V; x += att . ca_to_out^T           (same kernels, k_add)
+ *            x  += (att . sa_to_out^T) * sigmoid(1 - gate)          k_qgemm (GATE_RES epilogue)
+ *   cross:   h16 = rmsnorm(x, cross_norm); q = h16 . ca_to_q^T + q-norm (HEADS epilogue);
+ *            attention over the request's cached K/V; x += att . ca_to_out^T (+ local
+ *            cond)                                                  k_qgemm (ADD epilogue)
  *   ffn:     h16 = rmsnorm(x, ff_norm)*(1+scale)+shift
- *            GLU:  proj = h16 . ff_in^T + b; g16 = silu(gate)*value  k_qgemm (Q4), k_glu_combine
+ *            GLU:  g16 = silu(gate)*value of h16 . ff_in^T + b       k_qgemm (Q4, GLU epilogue)
  *            GELU: g16 = gelu(h16 . ff_in^T + b)                    k_qgemm with GELU epilogue
- *            x  += (g16 . ff_out^T + b) * sigmoid(1 - gate)         k_qgemm (Q4), k_gate_residual
+ *            x  += (g16 . ff_out^T + b) * sigmoid(1 - gate)         k_qgemm (Q4, GATE_RES epilogue)
  *
  * Nothing is allocated in the forward pass: every intermediate lives in the caller's
  * workspace (layout in ws_layout below).
@@ -144,7 +145,21 @@ aria_hip_dit_block *aria_hip_dit_block_create(const aria_dit_block_w *w, int dim
     if (!rc) rc = upv(&b->sa_k_norm, w->sa_k_norm, head_dim, acc);
     if (!rc) rc = upv(&b->ca_q_norm, w->ca_q_norm, head_dim, acc);
     if (!rc) rc = upv(&b->ca_k_norm, w->ca_k_norm, head_dim, acc);
-    if (!rc) rc = upv(&b->ff_in_b, w->ff_in_b, (size_t)b->ffrows, acc);
+    /* GLU: ff_in rows (and bias) are stored interleaved (value_i, gate_i) so the GEMM
+     * epilogue finds each pair in adjacent columns; rows are quantized independently, so
+     * the packed values are the reference quantizer's */
+    float *glu_w = NULL, *glu_b = NULL;
+    if (ffn == ARIA_FFN_GLU && w->ff_in_w) {
+        glu_w = (float *)malloc((size_t)2 * inner * dim * sizeof(float));
+        glu_b = w->ff_in_b ? (float *)malloc((size_t)2 * inner * sizeof(float)) : NULL;
+        if (!glu_w || (w->ff_in_b && !glu_b)) rc = ARIA_HIP_ENOMEM;
+        for (int i = 0; i < inner && !rc; i++) {
+            memcpy(glu_w + (size_t)(2 * i) * dim, w->ff_in_w + (size_t)i * dim, (size_t)dim * sizeof(float));
+            memcpy(glu_w + (size_t)(2 * i + 1) * dim, w->ff_in_w + (size_t)(inner + i) * dim, (size_t)dim * sizeof(float));
+            if (glu_b) { glu_b[2 * i] = w->ff_in_b[i]; glu_b[2 * i + 1] = w->ff_in_b[inner + i]; }
+        }
+    }
+    if (!rc) rc = upv(&b->ff_in_b, glu_w ? glu_b : w->ff_in_b, (size_t)b->ffrows, acc);
     if (!rc) rc = upv(&b->ff_out_b, w->ff_out_b, dim, acc);
     if (!rc) rc = upv(&b->tssg, w->to_scale_shift_gate, (size_t)6 * dim, acc);
     if (!rc && !b->tssg) { aria_hip_set_error("to_scale_shift_gate missing"); rc = ARIA_HIP_EINVAL; }
@@ -153,7 +168,9 @@ aria_hip_dit_block *aria_hip_dit_block_create(const aria_dit_block_w *w, int dim
     if (!rc) rc = pack(&b->ca_q, w->ca_to_q, dim, dim, attn_t, s, acc);
     if (!rc) rc = pack(&b->ca_out, w->ca_to_out, dim, dim, attn_t, s, acc);
     if (!rc) rc = pack(&b->ca_kv, w->ca_to_kv, 2 * dim, dim_ctx, ARIA_WF16, s, acc);
-    if (!rc) rc = pack(&b->ff_in, w->ff_in_w, b->ffrows, dim, ffn_t, s, acc);
+    if (!rc) rc = pack(&b->ff_in, glu_w ? glu_w : w->ff_in_w, b->ffrows, dim, ffn_t, s, acc);
+    free(glu_w);
+    free(glu_b);
     if (!rc) rc = pack(&b->ff_out, w->ff_out_w, dim, inner, ffn_t, s, acc);
     if (rc) {
         aria_hip_dit_block_free(b);
@@ -175,10 +192,10 @@ static size_t al(size_t n) { return (n + WS_ALIGN - 1) & ~(size_t)(WS_ALIGN - 1)
 
 static size_t ws_layout(const aria_hip_dit_block *b, int B, int S, int Sc, char *base, wsl *w) {
     const size_t M = (size_t)B * S, d = (size_t)b->dim;
-    size_t big = M * 3 * d * 4;
-    if (b->ffn == ARIA_FFN_GLU && M * (size_t)b->ffrows * 4 > big) big = M * (size_t)b->ffrows * 4;
-    if ((size_t)B * Sc * 2 * d * 4 > big) big = (size_t)B * Sc * 2 * d * 4;
-    const size_t sz[9] = {M * d * 2, big, M * d * 2, M * d * 2, M * d * 2, M * d * 2, M * d * 4,
+    /* big: the per-request cross K/V projection [B*Sc, 2*dim] fp32; the block's own
+     * projections write through their fused epilogues (o is kept for layout only) */
+    const size_t big = (size_t)B * Sc * 2 * d * 4;
+    const size_t sz[9] = {M * d * 2, big, M * d * 2, M * d * 2, M * d * 2, M * d * 2, 0,
                           M * (size_t)b->inner * 2, (size_t)6 * B * d * 4};
     size_t off = 0, o[9];
     for (int i = 0; i < 9; i++) { o[i] = off; off += al(sz[i]); }
@@ -210,6 +227,26 @@ size_t aria_hip_dit_block_workspace_bytes(const aria_hip_dit_block *b, int B, in
 static hipError_t gemm(const dmat *m, void *y, int y_f16, const uint16_t *x16, const float *bias, int M, int gelu,
                        hipStream_t s) {
     return aria_k_qgemm_t(y, y_f16, x16, 1, m->wtype, m->q, m->scale, bias, M, m->K, m->N, 0, gelu, s);
+}
+/* the projection with a fused epilogue (residual stream updates, head preparation) */
+static hipError_t gemm_e(const dmat *m, float *y, const uint16_t *x16, const float *bias, int M,
+                         const aria_qgemm_epi *e, hipStream_t s) {
+    return aria_k_qgemm_e(y, 0, x16, 1, m->wtype, m->q, m->scale, bias, M, m->K, m->N, 0, 0, e, s);
+}
+static aria_qgemm_epi epi_heads(int S, int H, int nsec, const int *kind, uint16_t *const *dst, const float *const *w,
+                                const float *dcos, const float *dsin, int rot, float eps) {
+    aria_qgemm_epi e;
+    memset(&e, 0, sizeof e);
+    e.mode = ARIA_EPI_HEADS; e.rows_per_batch = S; e.heads = H; e.nsec = nsec;
+    for (int i = 0; i < nsec; i++) { e.kind[i] = kind[i]; e.dst[i] = dst[i]; e.w[i] = w[i]; }
+    e.cos_t = dcos; e.sin_t = dsin; e.rot = rot; e.eps = eps;
+    return e;
+}
+static aria_qgemm_epi epi_resid(int mode, int S, const float *gate, const float *add2) {
+    aria_qgemm_epi e;
+    memset(&e, 0, sizeof e);
+    e.mode = mode; e.rows_per_batch = S; e.gate = gate; e.add2 = add2;
+    return e;
 }
 
 int aria_hip_dit_block_cross_kv_dev(aria_hip_dit_block *b, const float *dctx, int B, int Sc, uint16_t *dk,
@@ -277,43 +314,51 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
     /* ---- self-attention ---- */
     STEP(aria_k_rownorm(w.h16, 1, dx, b->pre_norm, NULL, scale_self, shift_self, S, 0, 0, ARIA_NORM_RMS, M, d,
                         eps_norm, s), "k_rownorm (pre_norm + adaLN)");
-    STEP(gemm(&b->sa_qkv, w.big, 0, w.h16, NULL, M, 0, s), "k_qgemm (sa_to_qkv)");
-    {
+    {   /* qkv projection with q/k RMSNorm + RoPE and the head split in its epilogue */
         const int kind[3] = {0, 1, 2};
         uint16_t *dst[3] = {w.q16, w.k16, w.v16};
         const float *nw[3] = {b->sa_q_norm, b->sa_k_norm, NULL};
-        STEP(aria_k_qkv_prep(w.big, 3 * d, B, S, H, 3, kind, dst, nw, dcos, dsin, rot, eps_qk, s), "k_qkv_prep");
+        const aria_qgemm_epi e = epi_heads(S, H, 3, kind, dst, nw, dcos, dsin, rot, eps_qk);
+        STEP(gemm_e(&b->sa_qkv, NULL, w.h16, NULL, M, &e, s), "k_qgemm (sa_to_qkv + heads)");
     }
     STEP(aria_k_flash_attn(w.q16, w.k16, w.v16, w.att16, 1, B * H, H, S, S, s), "k_flash_attn (self)");
-    STEP(gemm(&b->sa_out, w.o, 0, w.att16, NULL, M, 0, s), "k_qgemm (sa_to_out)");
-    STEP(aria_k_gate_residual(dx, dx, w.o, gate_self, NULL, M, d, S, s), "k_gate_residual (self)");
+    {   /* x += (att . sa_to_out^T) * sigmoid(1 - gate_self) */
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, gate_self, NULL);
+        STEP(gemm_e(&b->sa_out, dx, w.att16, NULL, M, &e, s), "k_qgemm (sa_to_out + gated residual)");
+    }
 
     /* ---- cross-attention (no RoPE, no gate) ---- */
     STEP(aria_k_rownorm(w.h16, 1, dx, b->cross_norm, NULL, NULL, NULL, 0, 0, 0, ARIA_NORM_RMS, M, d, eps_norm, s),
          "k_rownorm (cross_norm)");
-    STEP(gemm(&b->ca_q, w.big, 0, w.h16, NULL, M, 0, s), "k_qgemm (ca_to_q)");
     {
         const int kind[1] = {0};
         uint16_t *dst[1] = {w.q16};
         const float *nw[1] = {b->ca_q_norm};
-        STEP(aria_k_qkv_prep(w.big, d, B, S, H, 1, kind, dst, nw, NULL, NULL, 0, eps_qk, s), "k_qkv_prep (cross q)");
+        const aria_qgemm_epi e = epi_heads(S, H, 1, kind, dst, nw, NULL, NULL, 0, eps_qk);
+        STEP(gemm_e(&b->ca_q, NULL, w.h16, NULL, M, &e, s), "k_qgemm (ca_to_q + heads)");
     }
     STEP(aria_k_flash_attn(w.q16, dk, dv, w.att16, 1, B * H, H, S, Sc, s), "k_flash_attn (cross)");
-    STEP(gemm(&b->ca_out, w.o, 0, w.att16, NULL, M, 0, s), "k_qgemm (ca_to_out)");
-    STEP(aria_k_add(dx, dx, w.o, (size_t)M * d, s), "k_add (cross residual)");
-    if (dlocal) STEP(aria_k_add(dx, dx, dlocal, (size_t)M * d, s), "k_add (local cond)");
+    {   /* x += att . ca_to_out^T, then the local-additive cond (src/aria_sa3_dit.c:242-252) */
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_ADD, S, NULL, dlocal);
+        STEP(gemm_e(&b->ca_out, dx, w.att16, NULL, M, &e, s), "k_qgemm (ca_to_out + residual)");
+    }
 
     /* ---- feed-forward ---- */
     STEP(aria_k_rownorm(w.h16, 1, dx, b->ff_norm, NULL, scale_ff, shift_ff, S, 0, 0, ARIA_NORM_RMS, M, d, eps_norm, s),
          "k_rownorm (ff_norm + adaLN)");
-    if (b->ffn == ARIA_FFN_GLU) {
-        STEP(gemm(&b->ff_in, w.big, 0, w.h16, b->ff_in_b, M, 0, s), "k_qgemm (ff_in)");
-        STEP(aria_k_glu_combine(w.ff16, 1, w.big, NULL, M, b->inner, s), "k_glu_combine");
+    if (b->ffn == ARIA_FFN_GLU) {   /* g16 = silu(gate) * value in the projection's epilogue */
+        aria_qgemm_epi e;
+        memset(&e, 0, sizeof e);
+        e.mode = ARIA_EPI_GLU;
+        STEP(aria_k_qgemm_e(w.ff16, 1, w.h16, 1, b->ff_in.wtype, b->ff_in.q, b->ff_in.scale, b->ff_in_b, M,
+                            b->ff_in.K, b->ff_in.N, 0, 0, &e, s), "k_qgemm (ff_in + GLU)");
     } else {
         STEP(gemm(&b->ff_in, w.ff16, 1, w.h16, b->ff_in_b, M, 1, s), "k_qgemm (ff_in + GELU)");
     }
-    STEP(gemm(&b->ff_out, w.o, 0, w.ff16, NULL, M, 0, s), "k_qgemm (ff_out)");
-    STEP(aria_k_gate_residual(dx, dx, w.o, gate_ff, b->ff_out_b, M, d, S, s), "k_gate_residual (ff)");
+    {   /* x += (g16 . ff_out^T + b) * sigmoid(1 - gate_ff) */
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, gate_ff, NULL);
+        STEP(gemm_e(&b->ff_out, dx, w.ff16, b->ff_out_b, M, &e, s), "k_qgemm (ff_out + gated residual)");
+    }
     return 0;
 }
 

@@ -85,6 +85,27 @@ hipError_t aria_k_q4_dequant(float *W, const uint8_t *q, const float *scale, int
  * [N, 2*ceil(K/32)] as [min, step] pairs), ARIA_WF16 (q = fp16 W [N,K], scale unused).
  * x is fp32 or fp16 (x_f16), y fp32 or fp16 (y_f16). */
 enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2 };
+/* Fused epilogues, applied to v = acc * scale (+ bias) (GELU'd when gelu != 0):
+ *   STORE     y = v (fp32 or fp16)
+ *   GATE_RES  y = y + v * sigmoid(1 - gate[row / rows_per_batch][col])   (fp32, in place)
+ *   ADD       y = (y + v) (+ add2)                                        (fp32, in place)
+ *   HEADS     the N columns are nsec sections of heads*64: each 64-column head is
+ *             RMS-normalised (w, statistic in double) and rotated (RoPE rot dims) for
+ *             kinds 0/1, copied for kind 2, and written fp16 to dst[sec] as
+ *             [batch, heads, rows_per_batch, 64] (y unused)
+ *   GLU       columns interleave (value, gate) pairs: y[m][c/2] = silu(gate) * value,
+ *             fp16 [M, N/2] (the weight rows were interleaved when packed) */
+enum { ARIA_EPI_STORE = 0, ARIA_EPI_GATE_RES = 1, ARIA_EPI_ADD = 2, ARIA_EPI_HEADS = 3, ARIA_EPI_GLU = 4 };
+typedef struct {
+    int mode, rows_per_batch;
+    const float *gate, *add2;
+    int heads, nsec, kind[3];
+    uint16_t *dst[3];
+    const float *w[3];
+    const float *cos_t, *sin_t;
+    int rot;
+    float eps;
+} aria_qgemm_epi;
 hipError_t aria_k_qgemm(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                         const float *scale, const float *bias, int M, int K, int N, hipStream_t s);
 /* the same with an explicit workgroup tile: 1 = 128x128, 2 = 128x64, 3 = 64x128,
@@ -92,6 +113,10 @@ hipError_t aria_k_qgemm(void *y, int y_f16, const void *x, int x_f16, int wtype,
 hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                           const float *scale, const float *bias, int M, int K, int N, int tiles,
                           int gelu, hipStream_t s);
+/* the same with a fused epilogue (epi NULL = STORE); HEADS needs N % 64 == 0 */
+hipError_t aria_k_qgemm_e(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
+                          const float *scale, const float *bias, int M, int K, int N, int tiles,
+                          int gelu, const aria_qgemm_epi *epi, hipStream_t s);
 
 /* Attention (k_attn.hip). Head preparation: src [B*S, ld] fp32 holds nsec sections of
  * H*64 columns; kind[i] = 0 (q: RMSNorm w[i] + RoPE), 1 (k: same), 2 (v: copy); each

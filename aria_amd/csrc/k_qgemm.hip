@@ -42,6 +42,8 @@
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
 
+#include <cstring>
+
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
@@ -57,6 +59,7 @@ struct QArgs {
     int y_f16;
     int nblk;
     int gelu;   /* epilogue: y = gelu_tanh(acc*scale + b) (the config FFN's activation) */
+    aria_qgemm_epi epi;
 };
 
 #define BK 32          /* k per slice */
@@ -94,6 +97,9 @@ template <int FM_, int FN_, int WGM_, int WGN_>
 struct Cfg {
     static constexpr int FM = FM_, FN = FN_, WGM = WGM_, WGN = WGN_;
     static constexpr int BM = 32 * FM * WGM, BN = 32 * FN * WGN, NT = 64 * WGM * WGN;
+    /* workgroups per CU the register allocation must allow (two waves per SIMD, except
+     * the 128-accumulator 128x256 tile, which runs one) */
+    static constexpr int MINB = FM * FN >= 8 ? 1 : 2;
     /* epilogue staging: per wave 32 rows x 32*FN fp32, rows padded by 16 B */
     static constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
     static constexpr int TILE_BYTES = 2 * (BM + BN) * LDS_STRIDE * 2, EPI_BYTES = 4 * 32 * EPI_STRIDE;
@@ -211,8 +217,52 @@ __device__ __forceinline__ int xcd_tile(int g, int T) {
     return (g & 7) * per + (g >> 3);
 }
 
+/* HEADS epilogue for one lane: v holds columns nb..nb+3 of row m; the 16 lanes of a
+ * 64-column head are consecutive and share m (the wave's column range is head-aligned).
+ * The arithmetic is k_qkv_prep's (k_attn.hip): RMS statistic in double over the head,
+ * (x * inv) * w, then rotate-half RoPE over the first rot dims. */
+__device__ __forceinline__ void epi_heads(const QArgs &a, float *v, int m, int nb, int lane, bool ok) {
+    const aria_qgemm_epi &e = a.epi;
+    const int secw = e.heads * 64;
+    const int sec = min(nb / secw, e.nsec - 1), h = (nb % secw) >> 6, l = lane & 15;
+    const int S = e.rows_per_batch, s = m % S, b = m / S;
+    const int kind = e.kind[sec];
+    if (kind != 2) {
+        double ss = ((double)v[0] * v[0] + (double)v[1] * v[1]) + ((double)v[2] * v[2] + (double)v[3] * v[3]);
+        ss = grp_sum<16>(ss);
+        const float inv = (float)(1.0 / sqrt(ss / 64 + (double)e.eps));
+        const float *w = e.w[sec];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            v[k] = v[k] * inv;
+            if (w) v[k] = v[k] * w[4 * l + k];
+        }
+        if (e.rot > 0 && e.cos_t) {
+            const int rh = e.rot >> 1, lp = rh >> 2;   /* partner lane offset */
+            float p[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) p[k] = __shfl(v[k], (lane & 48) | (l ^ lp), ARIA_WAVE);
+            const int d0 = 4 * l;
+            if (d0 < e.rot) {
+                const bool first = d0 < rh;
+                const int i0 = first ? d0 : d0 - rh;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float c = e.cos_t[(size_t)s * rh + i0 + k], sn = e.sin_t[(size_t)s * rh + i0 + k];
+                    if (first) { float ac = v[k] * c, bs = p[k] * sn; v[k] = ac - bs; }
+                    else { float bc = v[k] * c, as = p[k] * sn; v[k] = bc + as; }
+                }
+            }
+        }
+    }
+    if (ok) {
+        uint16_t *d = e.dst[sec] + (((size_t)b * e.heads + h) * S + s) * 64 + 4 * l;
+        *reinterpret_cast<uint2 *>(d) = make_uint2(pack2h(v[0], v[1]), pack2h(v[2], v[3]));
+    }
+}
+
 template <class C, int WT, bool AF16>
-__global__ __launch_bounds__(C::NT) void k_qgemm_mfma(QArgs a, int NTN, int T) {
+__global__ __launch_bounds__(C::NT, C::MINB) void k_qgemm_mfma(QArgs a, int NTN, int T) {
     using TL = Tile<C, WT, AF16>;
     using S = typename TL::S;
     constexpr int FM = C::FM, FN = C::FN, BM = C::BM, BN = C::BN;
@@ -323,7 +373,7 @@ __global__ __launch_bounds__(C::NT) void k_qgemm_mfma(QArgs a, int NTN, int T) {
             const int m = tl.m0 + wm * 32 * FM + i * 32 + r;
             const float4 v4 = *reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(E) +
                                                                 r * C::EPI_STRIDE + ecol * 4);
-            if (m >= a.M || nb >= a.N) continue;
+            const bool ok = m < a.M && nb < a.N;
             float v[4] = {v4.x, v4.y, v4.z, v4.w};
             const float scv[4] = {sc.x, sc.y, sc.z, sc.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
 #pragma unroll
@@ -332,11 +382,37 @@ __global__ __launch_bounds__(C::NT) void k_qgemm_mfma(QArgs a, int NTN, int T) {
                 if (a.bias) v[e] = v[e] + bv[e];
                 if (a.gelu) v[e] = gelu_tanh_f(v[e]);
             }
-            if (a.y_f16)
+            if (a.epi.mode == ARIA_EPI_HEADS) {
+                if constexpr (LPR % 16 == 0) epi_heads(a, v, m, nb, lane, ok);
+                continue;
+            }
+            if (!ok) continue;
+            if (a.epi.mode == ARIA_EPI_GLU) {   /* (value, gate) pairs -> silu(gate) * value, fp16 */
+                *reinterpret_cast<uint32_t *>((uint16_t *)a.y + (size_t)m * (a.N >> 1) + (nb >> 1)) =
+                    pack2h(silu_f(v[1]) * v[0], silu_f(v[3]) * v[2]);
+                continue;
+            }
+            float *yf = (float *)a.y + (size_t)m * a.N + nb;
+            if (a.epi.mode == ARIA_EPI_GATE_RES) {
+                /* y += v * sigmoid(1 - gate): the rounding order of k_gate_residual */
+                const float4 rr = *reinterpret_cast<const float4 *>(yf);
+                const float4 gg = *reinterpret_cast<const float4 *>(a.epi.gate + (size_t)(m / a.epi.rows_per_batch) * a.N + nb);
+                *reinterpret_cast<float4 *>(yf) = make_float4(rr.x + v[0] * gate_sig_f(gg.x), rr.y + v[1] * gate_sig_f(gg.y),
+                                                              rr.z + v[2] * gate_sig_f(gg.z), rr.w + v[3] * gate_sig_f(gg.w));
+            } else if (a.epi.mode == ARIA_EPI_ADD) {
+                float4 rr = *reinterpret_cast<const float4 *>(yf);
+                rr = make_float4(rr.x + v[0], rr.y + v[1], rr.z + v[2], rr.w + v[3]);
+                if (a.epi.add2) {
+                    const float4 l2 = *reinterpret_cast<const float4 *>(a.epi.add2 + (size_t)m * a.N + nb);
+                    rr = make_float4(rr.x + l2.x, rr.y + l2.y, rr.z + l2.z, rr.w + l2.w);
+                }
+                *reinterpret_cast<float4 *>(yf) = rr;
+            } else if (a.y_f16) {
                 *reinterpret_cast<uint2 *>((uint16_t *)a.y + (size_t)m * a.N + nb) =
                     make_uint2(pack2h(v[0], v[1]), pack2h(v[2], v[3]));
-            else
-                *reinterpret_cast<float4 *>((float *)a.y + (size_t)m * a.N + nb) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                *reinterpret_cast<float4 *>(yf) = make_float4(v[0], v[1], v[2], v[3]);
+            }
         }
         __builtin_amdgcn_wave_barrier();
     }
@@ -422,21 +498,25 @@ using C8 = Cfg<1, 1, 2, 2>;   /*  64 x  64 */
 #define NCFG 8
 static const int cfg_bm[NCFG] = {192, 128, 96, 96, 128, 64, 128, 64};
 static const int cfg_bn[NCFG] = {128, 128, 256, 128, 256, 128, 64, 64};
+static const int cfg_fn[NCFG] = {2, 2, 2, 1, 4, 2, 1, 1};   /* 32x32 blocks per wave along n */
 
-/* Tile shape from the shape: a CU holds several workgroups at once, so the busiest CU
- * carries ceil(tiles / 256) tiles; cost = that count x the tile's MFMA work / the tile's
- * measured efficiency (bigger wave tiles read less LDS per MFMA; the 128x256 tile runs
- * one wave per SIMD). */
-static int pick_tiles(int M, int N) {
-    static const double eff[NCFG] = {1.0, 0.95, 0.9, 0.85, 0.8, 0.8, 0.8, 0.75};
-    double best = 1e300;
-    int bi = 1;
-    for (int i = 0; i < NCFG; i++) {
+/* Tile shape from the shape (measured on MI355X at the DiT's shapes): the largest tile
+ * that still gives every CU about two workgroups wins (per-tile efficiency grows with
+ * the tile, but a tile count near the CU count leaves CUs idle at the tail); when none
+ * does, the one with the most tiles. Order of preference: 192x128, 128x128, 64x128 /
+ * 128x64, 64x64. HEADS epilogues need a 64-column head inside one wave (FN >= 2). */
+static int pick_tiles(int M, int N, bool heads) {
+    static const int order[5] = {0, 1, 5, 6, 7};
+    int most = -1;
+    long most_t = -1;
+    for (int k = 0; k < 5; k++) {
+        const int i = order[k];
+        if (heads && cfg_fn[i] < 2) continue;   /* a head's 64 columns must sit in one wave */
         const long T = (long)((M + cfg_bm[i] - 1) / cfg_bm[i]) * ((N + cfg_bn[i] - 1) / cfg_bn[i]);
-        const double cost = (double)((T + 255) / 256) * cfg_bm[i] * cfg_bn[i] / eff[i];
-        if (cost < best - 1e-9) { best = cost; bi = i; }
+        if (T >= 384) return i;
+        if (T > most_t) { most_t = T; most = i; }
     }
-    return bi;
+    return most;
 }
 
 template <int WT, bool AF16>
@@ -447,15 +527,18 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
                          (WT != ARIA_WQ8 || ((uintptr_t)a.scale & 15u) == 0) &&
                          (WT != ARIA_WQ4 || ((uintptr_t)a.scale & 7u) == 0);
     if (!aligned) {
+        if (a.epi.mode != ARIA_EPI_STORE) return hipErrorInvalidValue;   /* fused epilogues need the MFMA path */
         dim3 grid((a.N + 63) / 64, (a.M + 63) / 64);
         hipLaunchKernelGGL((k_qgemm_simt<WT, AF16>), grid, dim3(256), 0, s, a);
         return hipGetLastError();
     }
     if constexpr (!AF16) {   /* fp32 activations: the fallback when no fp16 staging buffer was available */
+        if (a.epi.mode == ARIA_EPI_HEADS) return hipErrorInvalidValue;
         launch_cfg<C2, WT, AF16>(a, s);
         return hipGetLastError();
     } else {
-    const int c = (tiles >= 1 && tiles <= NCFG) ? tiles - 1 : pick_tiles(a.M, a.N);
+    int c = (tiles >= 1 && tiles <= NCFG) ? tiles - 1 : pick_tiles(a.M, a.N, a.epi.mode == ARIA_EPI_HEADS);
+    if (a.epi.mode == ARIA_EPI_HEADS && cfg_fn[c] < 2) c = pick_tiles(a.M, a.N, true);
     switch (c) {
         case 0: launch_cfg<C1, WT, AF16>(a, s); break;
         case 1: launch_cfg<C2, WT, AF16>(a, s); break;
@@ -470,18 +553,35 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
     }
 }
 
-extern "C" hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
+extern "C" hipError_t aria_k_qgemm_e(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                                      const float *scale, const float *bias, int M, int K, int N, int tiles,
-                                     int gelu, hipStream_t s) {
+                                     int gelu, const aria_qgemm_epi *epi, hipStream_t s) {
     if (M <= 0 || N <= 0) return hipSuccess;
     QArgs a;
     a.y = y; a.x = x; a.q = q; a.scale = scale; a.bias = bias;
     a.M = M; a.K = K; a.N = N; a.y_f16 = y_f16; a.nblk = (K + 31) / 32; a.gelu = gelu;
+    if (epi) a.epi = *epi;
+    else { memset(&a.epi, 0, sizeof a.epi); a.epi.mode = ARIA_EPI_STORE; }
+    if (a.epi.mode == ARIA_EPI_HEADS) {
+        if (N % 64 || a.epi.nsec < 1 || a.epi.nsec > 3 || a.epi.heads * 64 * a.epi.nsec != N ||
+            a.epi.rows_per_batch <= 0 || (a.epi.rot && (a.epi.rot > 64 || (a.epi.rot & 7)))) return hipErrorInvalidValue;
+        a.y = (void *)a.epi.dst[0];   /* alignment check only; y is not written */
+    } else if (a.epi.mode == ARIA_EPI_GLU) {
+        if (N % 4 || a.gelu) return hipErrorInvalidValue;
+    } else if (a.epi.mode != ARIA_EPI_STORE) {
+        if (y_f16 || a.epi.rows_per_batch <= 0) return hipErrorInvalidValue;
+    }
     if (wtype == ARIA_WQ8) return x_f16 ? launch_q<ARIA_WQ8, true>(a, tiles, s) : launch_q<ARIA_WQ8, false>(a, tiles, s);
     if (wtype == ARIA_WQ4) return x_f16 ? launch_q<ARIA_WQ4, true>(a, tiles, s) : launch_q<ARIA_WQ4, false>(a, tiles, s);
     if (wtype == ARIA_WF16)
         return x_f16 ? launch_q<ARIA_WF16, true>(a, tiles, s) : launch_q<ARIA_WF16, false>(a, tiles, s);
     return hipErrorInvalidValue;
+}
+
+extern "C" hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
+                                     const float *scale, const float *bias, int M, int K, int N, int tiles,
+                                     int gelu, hipStream_t s) {
+    return aria_k_qgemm_e(y, y_f16, x, x_f16, wtype, q, scale, bias, M, K, N, tiles, gelu, nullptr, s);
 }
 
 extern "C" hipError_t aria_k_qgemm(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
