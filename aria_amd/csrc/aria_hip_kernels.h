@@ -108,8 +108,10 @@ typedef struct {
 } aria_qgemm_epi;
 hipError_t aria_k_qgemm(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                         const float *scale, const float *bias, int M, int K, int N, hipStream_t s);
-/* the same with an explicit workgroup tile: 1 = 128x128, 2 = 128x64, 3 = 64x128,
- * 4 = 64x64 (M x N); 0 = picked from the shape; gelu != 0 applies tanh-GELU after bias */
+/* the same with an explicit workgroup tile (M x N): 1..8 = the LDS-operand kernel's
+ * 192x128, 128x128, 96x256, 96x128, 128x256, 64x128, 128x64, 64x64; 9..12 = the
+ * weights-in-registers kernel's 32x256 .. 128x256 (Q8/Q4, K % 64 == 0); 0 = picked from
+ * the shape; gelu != 0 applies tanh-GELU after bias */
 hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                           const float *scale, const float *bias, int M, int K, int N, int tiles,
                           int gelu, hipStream_t s);

@@ -39,28 +39,7 @@
  * Shapes with K % 32 != 0, N % 4 != 0 or unaligned operands take a SIMT fp32 kernel with
  * the same dequant values (k_qgemm_simt).
  */
-#include "aria_dev.h"
-#include "aria_hip_kernels.h"
-
-#include <cstring>
-
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef float float2_t __attribute__((ext_vector_type(2)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-struct QArgs {
-    void *y;
-    const void *x;
-    const void *q;
-    const float *scale;
-    const float *bias;
-    int M, K, N;
-    int y_f16;
-    int nblk;
-    int gelu;   /* epilogue: y = gelu_tanh(acc*scale + b) (the config FFN's activation) */
-    aria_qgemm_epi epi;
-};
+#include "qgemm_dev.h"
 
 #define BK 32          /* k per slice */
 #define LDS_STRIDE 32  /* halves per LDS row: 64 B, 4 chunks of 8 k */
@@ -74,22 +53,6 @@ __device__ __forceinline__ int lds_off(int row, int chunk) { return row * LDS_ST
 /* producer slot c -> (row, chunk), row-major */
 __device__ __forceinline__ int slot_row(int c) { return c >> 2; }
 __device__ __forceinline__ int slot_chunk(int c) { return c & 3; }
-
-/* two fp32 -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32) */
-__device__ __forceinline__ uint32_t pack2h(float a, float b) {
-    const float2_t f = {a, b};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));
-}
-
-/* Q8: four int8 in one word -> two words of fp16 pairs, exactly. Each byte is biased to
- * unsigned (b ^ 0x80 = b + 128) and placed under the fp16 exponent of 1024
- * (0x64XX = 1024 + XX), then 1152 is subtracted: an exact integer in [-127, 127]. */
-__device__ __forceinline__ void q8x4_to_h(uint32_t w, uint32_t &lo, uint32_t &hi) {
-    const uint32_t u = w ^ 0x80808080u;
-    const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
-}
 
 /* ---- tile configuration: a 2-D grid of WGM x WGN waves, each owning FM x FN 32x32
  * blocks (FM along the activation rows m, FN along the weight rows n) ---- */
@@ -208,59 +171,6 @@ struct Tile {
     }
 };
 
-/* Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
- * workgroup g runs on XCD g % 8. Tile t = (g % 8) * ceil(T/8) + g / 8 gives each
- * XCD a contiguous run of tiles in M-major order, so an XCD's L2 holds a few
- * activation row panels and the weight panels instead of every activation row. */
-__device__ __forceinline__ int xcd_tile(int g, int T) {
-    const int per = (T + 7) >> 3;
-    return (g & 7) * per + (g >> 3);
-}
-
-/* HEADS epilogue for one lane: v holds columns nb..nb+3 of row m; the 16 lanes of a
- * 64-column head are consecutive and share m (the wave's column range is head-aligned).
- * The arithmetic is k_qkv_prep's (k_attn.hip): RMS statistic in double over the head,
- * (x * inv) * w, then rotate-half RoPE over the first rot dims. */
-__device__ __forceinline__ void epi_heads(const QArgs &a, float *v, int m, int nb, int lane, bool ok) {
-    const aria_qgemm_epi &e = a.epi;
-    const int secw = e.heads * 64;
-    const int sec = min(nb / secw, e.nsec - 1), h = (nb % secw) >> 6, l = lane & 15;
-    const int S = e.rows_per_batch, s = m % S, b = m / S;
-    const int kind = e.kind[sec];
-    if (kind != 2) {
-        double ss = ((double)v[0] * v[0] + (double)v[1] * v[1]) + ((double)v[2] * v[2] + (double)v[3] * v[3]);
-        ss = grp_sum<16>(ss);
-        const float inv = (float)(1.0 / sqrt(ss / 64 + (double)e.eps));
-        const float *w = e.w[sec];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            v[k] = v[k] * inv;
-            if (w) v[k] = v[k] * w[4 * l + k];
-        }
-        if (e.rot > 0 && e.cos_t) {
-            const int rh = e.rot >> 1, lp = rh >> 2;   /* partner lane offset */
-            float p[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) p[k] = __shfl(v[k], (lane & 48) | (l ^ lp), ARIA_WAVE);
-            const int d0 = 4 * l;
-            if (d0 < e.rot) {
-                const bool first = d0 < rh;
-                const int i0 = first ? d0 : d0 - rh;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const float c = e.cos_t[(size_t)s * rh + i0 + k], sn = e.sin_t[(size_t)s * rh + i0 + k];
-                    if (first) { float ac = v[k] * c, bs = p[k] * sn; v[k] = ac - bs; }
-                    else { float bc = v[k] * c, as = p[k] * sn; v[k] = bc + as; }
-                }
-            }
-        }
-    }
-    if (ok) {
-        uint16_t *d = e.dst[sec] + (((size_t)b * e.heads + h) * S + s) * 64 + 4 * l;
-        *reinterpret_cast<uint2 *>(d) = make_uint2(pack2h(v[0], v[1]), pack2h(v[2], v[3]));
-    }
-}
-
 template <class C, int WT, bool AF16>
 __global__ __launch_bounds__(C::NT, C::MINB) void k_qgemm_mfma(QArgs a, int NTN, int T) {
     using TL = Tile<C, WT, AF16>;
@@ -342,80 +252,9 @@ __global__ __launch_bounds__(C::NT, C::MINB) void k_qgemm_mfma(QArgs a, int NTN,
     if (kt < KT) step(kt, s1, s0);
     if (kt + 1 < KT) step(kt + 1, s2, s1);
 
-    /* epilogue: each wave stages 32 rows of its tile at a time through LDS (fp32, rows
-     * padded), then writes whole row segments: 16 lanes x 16 B per row, coalesced.
-     * acc register r of lane l -> n = 8*(r/4) + 4*(l/32) + r%4, m = l%32 in its block.
-     * The last slice's barrier has released the tile buffers. */
+    /* the last slice's barrier has released the tile buffers */
     float *E = reinterpret_cast<float *>(lds) + wave * (32 * C::EPI_STRIDE / 4);
-    constexpr int CW = 32 * FN;                 /* columns per wave */
-    constexpr int LPR = CW / 4;                 /* lanes per row (16 B each) */
-    constexpr int RPI = 64 / LPR;               /* rows per store instruction */
-    const int ecol = (lane % LPR) * 4, erow = lane / LPR;
-    const int nb = tl.n0 + wn * CW + ecol;      /* this lane's 4 output columns */
-    float4 sc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), bb = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (nb < a.N) {
-        if (WT == ARIA_WQ8) sc = *reinterpret_cast<const float4 *>(a.scale + nb);
-        if (a.bias) bb = *reinterpret_cast<const float4 *>(a.bias + nb);
-    }
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-#pragma unroll
-        for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int g = 0; g < 4; g++)
-                *reinterpret_cast<float4 *>(reinterpret_cast<char *>(E) + lrow * C::EPI_STRIDE +
-                                            (j * 32 + 8 * g + 4 * lh) * 4) =
-                    make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int it = 0; it < 32 / RPI; it++) {
-            const int r = it * RPI + erow;
-            const int m = tl.m0 + wm * 32 * FM + i * 32 + r;
-            const float4 v4 = *reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(E) +
-                                                                r * C::EPI_STRIDE + ecol * 4);
-            const bool ok = m < a.M && nb < a.N;
-            float v[4] = {v4.x, v4.y, v4.z, v4.w};
-            const float scv[4] = {sc.x, sc.y, sc.z, sc.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                if (WT == ARIA_WQ8) v[e] = v[e] * scv[e];
-                if (a.bias) v[e] = v[e] + bv[e];
-                if (a.gelu) v[e] = gelu_tanh_f(v[e]);
-            }
-            if (a.epi.mode == ARIA_EPI_HEADS) {
-                if constexpr (LPR % 16 == 0) epi_heads(a, v, m, nb, lane, ok);
-                continue;
-            }
-            if (!ok) continue;
-            if (a.epi.mode == ARIA_EPI_GLU) {   /* (value, gate) pairs -> silu(gate) * value, fp16 */
-                *reinterpret_cast<uint32_t *>((uint16_t *)a.y + (size_t)m * (a.N >> 1) + (nb >> 1)) =
-                    pack2h(silu_f(v[1]) * v[0], silu_f(v[3]) * v[2]);
-                continue;
-            }
-            float *yf = (float *)a.y + (size_t)m * a.N + nb;
-            if (a.epi.mode == ARIA_EPI_GATE_RES) {
-                /* y += v * sigmoid(1 - gate): the rounding order of k_gate_residual */
-                const float4 rr = *reinterpret_cast<const float4 *>(yf);
-                const float4 gg = *reinterpret_cast<const float4 *>(a.epi.gate + (size_t)(m / a.epi.rows_per_batch) * a.N + nb);
-                *reinterpret_cast<float4 *>(yf) = make_float4(rr.x + v[0] * gate_sig_f(gg.x), rr.y + v[1] * gate_sig_f(gg.y),
-                                                              rr.z + v[2] * gate_sig_f(gg.z), rr.w + v[3] * gate_sig_f(gg.w));
-            } else if (a.epi.mode == ARIA_EPI_ADD) {
-                float4 rr = *reinterpret_cast<const float4 *>(yf);
-                rr = make_float4(rr.x + v[0], rr.y + v[1], rr.z + v[2], rr.w + v[3]);
-                if (a.epi.add2) {
-                    const float4 l2 = *reinterpret_cast<const float4 *>(a.epi.add2 + (size_t)m * a.N + nb);
-                    rr = make_float4(rr.x + l2.x, rr.y + l2.y, rr.z + l2.z, rr.w + l2.w);
-                }
-                *reinterpret_cast<float4 *>(yf) = rr;
-            } else if (a.y_f16) {
-                *reinterpret_cast<uint2 *>((uint16_t *)a.y + (size_t)m * a.N + nb) =
-                    make_uint2(pack2h(v[0], v[1]), pack2h(v[2], v[3]));
-            } else {
-                *reinterpret_cast<float4 *>(yf) = make_float4(v[0], v[1], v[2], v[3]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-    }
+    epilogue<FM, FN, WT, EPI_ANY>(a, acc, E, lane, tl.m0 + wm * 32 * FM, tl.n0 + wn * 32 * FN);
 }
 
 /* ---- SIMT fallback: any K, any alignment; fp32 FMA on the dequantized values ---- */
@@ -519,6 +358,29 @@ static int pick_tiles(int M, int N, bool heads) {
     return most;
 }
 
+/* Weights-in-registers kernel pick (Q8/Q4, fp16 activations, K % 64 == 0): BM = 32 * FM
+ * rows by 256 weight rows per workgroup, FM = 1..4. Cost model fitted to MI355X sweeps of
+ * the DiT's GEMMs (M = 2592; N/K = 3072/1024, 1024/1024, 4096/1024, 1024/4096,
+ * 8192/1024): rounds of workgroups over 256 CUs (two resident per CU for FM <= 2) times
+ * the per-workgroup time, which grows with FM and with the workgroups sharing a CU,
+ * scaled by a per-FM efficiency (LDS and L1 traffic per MFMA fall with FM; FM = 4 runs one
+ * wave per SIMD and hides less latency). */
+static int pick_wr(int M, int N, int K) {
+    (void)K;
+    static const float eff[5] = {0.0f, 1.6f, 1.25f, 1.1f, 1.35f};
+    int best = 2;
+    float best_c = 1e30f;
+    for (int fm = 1; fm <= 4; fm++) {
+        const long T = (long)((M + 32 * fm - 1) / (32 * fm)) * ((N + 255) / 256);
+        const int occ = fm <= 2 ? 2 : 1;
+        const long rounds = (T + 256L * occ - 1) / (256L * occ);
+        const long share = T >= 256 * occ ? occ : (T + 255) / 256;   /* workgroups per CU at once */
+        const float c = (float)(rounds * fm * (share < 1 ? 1 : share)) * eff[fm];
+        if (c < best_c) { best_c = c; best = fm; }
+    }
+    return best;
+}
+
 template <int WT, bool AF16>
 static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
     const bool aligned = a.K % BK == 0 && a.N % 4 == 0 && ((uintptr_t)a.x & 15u) == 0 &&
@@ -537,6 +399,11 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
         launch_cfg<C2, WT, AF16>(a, s);
         return hipGetLastError();
     } else {
+    if constexpr (WT != ARIA_WF16) {
+        /* weights-in-registers kernel: explicit tiles 9..12 (BM = 32 * (tiles - 8)), or the pick */
+        const int fm = (tiles > NCFG) ? tiles - NCFG : (tiles == 0 ? pick_wr(a.M, a.N, a.K) : 0);
+        if (fm > 0 && a.K % 64 == 0) return qgemm_wr_launch(a, WT, fm, s);
+    }
     int c = (tiles >= 1 && tiles <= NCFG) ? tiles - 1 : pick_tiles(a.M, a.N, a.epi.mode == ARIA_EPI_HEADS);
     if (a.epi.mode == ARIA_EPI_HEADS && cfg_fn[c] < 2) c = pick_tiles(a.M, a.N, true);
     switch (c) {

@@ -1,0 +1,253 @@
+/*
+ * qgemm_dev.h - device code shared by the two dequant-on-use GEMM kernels
+ * (k_qgemm.hip: both operands staged through LDS; k_qgemm_wr.hip: weights loaded
+ * straight into registers): the kernel argument block, fp16 packing, the Q8 unpack,
+ * the XCD-aware tile order and the fused epilogue. Included by those two files only.
+ */
+#ifndef ARIA_QGEMM_DEV_H
+#define ARIA_QGEMM_DEV_H
+
+#include "aria_dev.h"
+#include "aria_hip_kernels.h"
+
+#include <cstring>
+#include <type_traits>
+
+template <int I>
+using IC = std::integral_constant<int, I>;
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+struct QArgs {
+    void *y;
+    const void *x;
+    const void *q;
+    const float *scale;
+    const float *bias;
+    int M, K, N;
+    int y_f16;
+    int nblk;
+    int gelu;   /* epilogue: y = gelu_tanh(acc*scale + b) (the config FFN's activation) */
+    aria_qgemm_epi epi;
+};
+
+/* two fp32 -> packed fp16 pair, round to nearest even (v_cvt_pk_f16_f32) */
+__device__ __forceinline__ uint32_t pack2h(float a, float b) {
+    const float2_t f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_t));
+}
+
+/* Q8: four int8 in one word -> two words of fp16 pairs, exactly. Each byte is biased to
+ * unsigned (b ^ 0x80 = b + 128) and placed under the fp16 exponent of 1024
+ * (0x64XX = 1024 + XX), then 1152 is subtracted: an exact integer in [-127, 127]. */
+__device__ __forceinline__ void q8x4_to_h(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
+}
+
+/* Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
+ * workgroup g runs on XCD g % 8. Tile t = (g % 8) * ceil(T/8) + g / 8 gives each
+ * XCD a contiguous run of tiles in M-major order, so an XCD's L2 holds a few
+ * activation row panels and the weight panels instead of every activation row. */
+__device__ __forceinline__ int xcd_tile(int g, int T) {
+    const int per = (T + 7) >> 3;
+    return (g & 7) * per + (g >> 3);
+}
+
+/* Epilogue of one wave: its FM x FN blocks of 32x32 accumulators are staged through
+ * LDS 32 rows at a time (fp32, rows padded by 16 B) and written as whole row segments:
+ * 16 B per lane, coalesced. acc register r of lane l holds n = 8*(r/4) + 4*(l/32) + r%4,
+ * m = l%32 of its block. E is this wave's staging area (32 rows of 32*FN*4 + 16 bytes);
+ * mw / nw are the first activation row and the first weight row of the wave's tile.
+ * v = acc * scale (Q8) + bias, GELU'd when a.gelu, then the fused mode MODE (compile
+ * time; EPI_ANY dispatches on a.epi.mode at run time). Every global load of a 32-row
+ * group (residual, gate, local cond, RoPE tables) is issued before its first store:
+ * loads and stores retire in order, so a load issued after a store would make the next
+ * wait cover that store's whole write latency.
+ * HEADS: the 16 lanes of a 64-column head share a row m (the wave's column range is
+ * head-aligned); the arithmetic is k_qkv_prep's (k_attn.hip): RMS statistic in double
+ * over the head, (x * inv) * w, then rotate-half RoPE over the first rot dims. */
+#define EPI_ANY (-1)
+template <int FM, int FN, int WT, int MODE>
+__device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN], float *E, int lane, int mw, int nw) {
+    constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
+    constexpr int CW = 32 * FN;                 /* columns per wave */
+    constexpr int LPR = CW / 4;                 /* lanes per row (16 B each) */
+    constexpr int RPI = 64 / LPR;               /* rows per store instruction */
+    constexpr int NIT = 32 / RPI;               /* store instructions per 32-row group */
+    if constexpr (MODE == EPI_ANY) {
+        switch (a.epi.mode) {
+            case ARIA_EPI_GATE_RES: epilogue<FM, FN, WT, ARIA_EPI_GATE_RES>(a, acc, E, lane, mw, nw); return;
+            case ARIA_EPI_ADD: epilogue<FM, FN, WT, ARIA_EPI_ADD>(a, acc, E, lane, mw, nw); return;
+            case ARIA_EPI_HEADS: if constexpr (LPR % 16 == 0) epilogue<FM, FN, WT, ARIA_EPI_HEADS>(a, acc, E, lane, mw, nw); return;
+            case ARIA_EPI_GLU: epilogue<FM, FN, WT, ARIA_EPI_GLU>(a, acc, E, lane, mw, nw); return;
+            default: epilogue<FM, FN, WT, ARIA_EPI_STORE>(a, acc, E, lane, mw, nw); return;
+        }
+    } else {
+    static_assert(MODE != ARIA_EPI_HEADS || LPR % 16 == 0, "a head's 64 columns must sit in one wave");
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int ecol = (lane % LPR) * 4, erow = lane / LPR;
+    const int nb = nw + ecol;                   /* this lane's 4 output columns */
+    const bool col_ok = nb < a.N;
+    float4 sc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), bb = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (col_ok) {
+        if (WT == ARIA_WQ8) sc = *reinterpret_cast<const float4 *>(a.scale + nb);
+        if (a.bias) bb = *reinterpret_cast<const float4 *>(a.bias + nb);
+    }
+    /* HEADS: per-lane constants of the epilogue (section, head, norm gains, RoPE lanes) */
+    const aria_qgemm_epi &e = a.epi;
+    int hh = 0, l16 = 0, kind = 2, rh = 0, i0 = 0;
+    bool rope = false, first = false;
+    float4 gw = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    uint16_t *dsec = nullptr;                   /* this lane's head section (kernel-argument
+                                                 * arrays indexed once, not per row) */
+    if constexpr (MODE == ARIA_EPI_HEADS) {
+        const int secw = e.heads * 64;
+        const int sec = min(nb / secw, e.nsec - 1);
+        hh = (nb % secw) >> 6;
+        l16 = lane & 15;
+        kind = e.kind[sec];
+        dsec = e.dst[sec];
+        const float *wsec = e.w[sec];
+        if (kind != 2 && wsec) gw = *reinterpret_cast<const float4 *>(wsec + 4 * l16);
+        rh = e.rot >> 1;
+        const int d0 = 4 * l16;
+        rope = kind != 2 && e.rot > 0 && e.cos_t && d0 < e.rot;
+        first = d0 < rh;
+        i0 = first ? d0 : d0 - rh;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<float4 *>(reinterpret_cast<char *>(E) + lrow * EPI_STRIDE +
+                                            (j * 32 + 8 * g + 4 * lh) * 4) =
+                    make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+        __builtin_amdgcn_wave_barrier();
+        float v[NIT][4];
+        int mrow[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int r = it * RPI + erow;
+            mrow[it] = mw + i * 32 + r;
+            const float4 v4 = *reinterpret_cast<const float4 *>(reinterpret_cast<const char *>(E) +
+                                                                r * EPI_STRIDE + ecol * 4);
+            v[it][0] = v4.x; v[it][1] = v4.y; v[it][2] = v4.z; v[it][3] = v4.w;
+            const float scv[4] = {sc.x, sc.y, sc.z, sc.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                if (WT == ARIA_WQ8) v[it][q] = v[it][q] * scv[q];
+                if (a.bias) v[it][q] = v[it][q] + bv[q];
+                if (a.gelu) v[it][q] = gelu_tanh_f(v[it][q]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();   /* staging reads done before the next group's writes */
+        if constexpr (MODE == ARIA_EPI_STORE) {
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                const int m = mrow[it];
+                if (m >= a.M || !col_ok) continue;
+                if (a.y_f16)
+                    *reinterpret_cast<uint2 *>((uint16_t *)a.y + (size_t)m * a.N + nb) =
+                        make_uint2(pack2h(v[it][0], v[it][1]), pack2h(v[it][2], v[it][3]));
+                else
+                    *reinterpret_cast<float4 *>((float *)a.y + (size_t)m * a.N + nb) =
+                        make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
+            }
+        } else if constexpr (MODE == ARIA_EPI_GLU) {   /* (value, gate) pairs -> silu(gate) * value, fp16 */
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                const int m = mrow[it];
+                if (m >= a.M || !col_ok) continue;
+                *reinterpret_cast<uint32_t *>((uint16_t *)a.y + (size_t)m * (a.N >> 1) + (nb >> 1)) =
+                    pack2h(silu_f(v[it][1]) * v[it][0], silu_f(v[it][3]) * v[it][2]);
+            }
+        } else if constexpr (MODE == ARIA_EPI_GATE_RES || MODE == ARIA_EPI_ADD) {
+            /* read-modify-write of the fp32 residual: all loads first, then all stores */
+            float4 rr[NIT], g2[NIT];
+            const int nbc = col_ok ? nb : 0;
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                const int mc = min(mrow[it], a.M - 1);
+                rr[it] = *reinterpret_cast<const float4 *>((const float *)a.y + (size_t)mc * a.N + nbc);
+                if (MODE == ARIA_EPI_GATE_RES)
+                    g2[it] = *reinterpret_cast<const float4 *>(e.gate + (size_t)(mc / e.rows_per_batch) * a.N + nbc);
+                else if (e.add2)
+                    g2[it] = *reinterpret_cast<const float4 *>(e.add2 + (size_t)mc * a.N + nbc);
+            }
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                const int m = mrow[it];
+                if (m >= a.M || !col_ok) continue;
+                float4 o;
+                if (MODE == ARIA_EPI_GATE_RES) {
+                    /* y += v * sigmoid(1 - gate): the rounding order of k_gate_residual */
+                    o = make_float4(rr[it].x + v[it][0] * gate_sig_f(g2[it].x), rr[it].y + v[it][1] * gate_sig_f(g2[it].y),
+                                    rr[it].z + v[it][2] * gate_sig_f(g2[it].z), rr[it].w + v[it][3] * gate_sig_f(g2[it].w));
+                } else {
+                    o = make_float4(rr[it].x + v[it][0], rr[it].y + v[it][1], rr[it].z + v[it][2], rr[it].w + v[it][3]);
+                    if (e.add2) o = make_float4(o.x + g2[it].x, o.y + g2[it].y, o.z + g2[it].z, o.w + g2[it].w);
+                }
+                *reinterpret_cast<float4 *>((float *)a.y + (size_t)m * a.N + nb) = o;
+            }
+        } else {   /* HEADS */
+            const int S = e.rows_per_batch;
+            float4 cs[NIT], sn[NIT];
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                if (rope) {
+                    const int s = min(mrow[it], a.M - 1) % S;
+                    cs[it] = *reinterpret_cast<const float4 *>(e.cos_t + (size_t)s * rh + i0);
+                    sn[it] = *reinterpret_cast<const float4 *>(e.sin_t + (size_t)s * rh + i0);
+                }
+            }
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                const int m = mrow[it];
+                float *w4 = v[it];
+                if (kind != 2) {
+                    double ss = ((double)w4[0] * w4[0] + (double)w4[1] * w4[1]) + ((double)w4[2] * w4[2] + (double)w4[3] * w4[3]);
+                    ss = grp_sum<16>(ss);
+                    const float inv = (float)(1.0 / sqrt(ss / 64 + (double)e.eps));
+                    const float gv[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+                    for (int q = 0; q < 4; q++) w4[q] = (w4[q] * inv) * gv[q];   /* gv = 1 without gains */
+                    if (e.rot > 0 && e.cos_t) {
+                        const int lp = rh >> 2;   /* partner lane offset */
+                        float p[4];
+#pragma unroll
+                        for (int q = 0; q < 4; q++) p[q] = __shfl(w4[q], (lane & 48) | (l16 ^ lp), ARIA_WAVE);
+                        if (rope) {
+                            const float cv[4] = {cs[it].x, cs[it].y, cs[it].z, cs[it].w};
+                            const float sv[4] = {sn[it].x, sn[it].y, sn[it].z, sn[it].w};
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                if (first) { float ac = w4[q] * cv[q], bs = p[q] * sv[q]; w4[q] = ac - bs; }
+                                else { float bc = w4[q] * cv[q], as = p[q] * sv[q]; w4[q] = bc + as; }
+                            }
+                        }
+                    }
+                }
+                if (m < a.M && col_ok) {
+                    const int s = m % S, b = m / S;
+                    uint16_t *d = dsec + (((size_t)b * e.heads + hh) * S + s) * 64 + 4 * l16;
+                    *reinterpret_cast<uint2 *>(d) = make_uint2(pack2h(w4[0], w4[1]), pack2h(w4[2], w4[3]));
+                }
+            }
+        }
+    }
+    }
+}
+
+/* the weights-in-registers kernel's launcher (k_qgemm_wr.hip): BM = 32 * fm rows by
+ * 256 weight rows per workgroup; wt is ARIA_WQ8 or ARIA_WQ4, activations fp16, K % 64 == 0 */
+hipError_t qgemm_wr_launch(const QArgs &a, int wt, int fm, hipStream_t s);
+
+#endif /* ARIA_QGEMM_DEV_H */

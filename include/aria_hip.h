@@ -136,9 +136,11 @@ int aria_hip_q4_dequant_dev(float *dW, const uint8_t *dq, const float *dscale, i
 int aria_hip_qlinear_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
                          const float *dscale, const float *db, int M, int K, int N, void *stream);
 /* As aria_hip_qlinear_dev with an explicit workgroup tile (M x N): 1 = 192x128,
- * 2 = 128x128, 3 = 96x256, 4 = 96x128, 5 = 128x256, 6 = 64x128, 7 = 128x64, 8 = 64x64,
- * 0 = chosen from the shape (tuning knob; fp32 activations without an fp16 staging
- * buffer always run 128x128). */
+ * 2 = 128x128, 3 = 96x256, 4 = 96x128, 5 = 128x256, 6 = 64x128, 7 = 128x64, 8 = 64x64
+ * (both operands staged through LDS); 9..12 = 32x256, 64x256, 96x256, 128x256 with the
+ * weights loaded straight into registers (Q8/Q4 with K % 64 == 0, else the 128x128 LDS
+ * kernel); 0 = chosen from the shape (tuning knob; fp32 activations without an fp16
+ * staging buffer always run 128x128). */
 int aria_hip_qlinear_ex_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
                             const float *dscale, const float *db, int M, int K, int N, int tiles,
                             void *stream);

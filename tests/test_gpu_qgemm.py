@@ -115,7 +115,7 @@ def test_qgemm_identity_weights(ops, port):
     assert relerr_max(y, x[:, perm]) <= GATE
 
 
-@pytest.mark.parametrize("tiles", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("tiles", [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("wtype", [0, 1])
 def test_qgemm_every_tile_shape(hip, port, tiles, wtype):
     """Each workgroup tile shape, with ragged M and N edges, fp32 and fp16 activations."""
