@@ -5,7 +5,8 @@
  * mixed-precision recipe, fp16 otherwise). The forward pass is the order of
  * dit_block_core (src/aria_sa3_dit.c:141-312), each step one gfx950 kernel:
  *
- *   mod      = to_scale_shift_gate + gcond, chunk-major            k_mod_chunks
+ *   modulation chunks (scale, shift, gate) = to_scale_shift_gate + gcond, formed in the
+ *            kernels that use them (the norm kernels and the gated-residual epilogues)
  *   self:    h16 = rmsnorm(x, pre_norm)*(1+scale)+shift  (fp16)    k_rownorm (fused adaLN)
  *            q,k,v = h16 . sa_to_qkv^T, split into heads, q/k rmsnorm + RoPE, fp16
  *            head-major                                             k_qgemm (Q8, HEADS epilogue)
@@ -184,7 +185,7 @@ size_t aria_hip_dit_block_weight_bytes(const aria_hip_dit_block *b) { return b ?
 /* ---- workspace ---- */
 typedef struct {
     uint16_t *h16, *q16, *k16, *v16, *att16, *ff16;
-    float *big, *o, *mod;
+    float *big, *o;
 } wsl;
 
 #define WS_ALIGN 256
@@ -195,10 +196,10 @@ static size_t ws_layout(const aria_hip_dit_block *b, int B, int S, int Sc, char 
     /* big: the per-request cross K/V projection [B*Sc, 2*dim] fp32; the block's own
      * projections write through their fused epilogues (o is kept for layout only) */
     const size_t big = (size_t)B * Sc * 2 * d * 4;
-    const size_t sz[9] = {M * d * 2, big, M * d * 2, M * d * 2, M * d * 2, M * d * 2, 0,
-                          M * (size_t)b->inner * 2, (size_t)6 * B * d * 4};
-    size_t off = 0, o[9];
-    for (int i = 0; i < 9; i++) { o[i] = off; off += al(sz[i]); }
+    const size_t sz[8] = {M * d * 2, big, M * d * 2, M * d * 2, M * d * 2, M * d * 2, 0,
+                          M * (size_t)b->inner * 2};
+    size_t off = 0, o[8];
+    for (int i = 0; i < 8; i++) { o[i] = off; off += al(sz[i]); }
     if (base && w) {
         w->h16 = (uint16_t *)(base + o[0]);
         w->big = (float *)(base + o[1]);
@@ -208,7 +209,6 @@ static size_t ws_layout(const aria_hip_dit_block *b, int B, int S, int Sc, char 
         w->att16 = (uint16_t *)(base + o[5]);
         w->o = (float *)(base + o[6]);
         w->ff16 = (uint16_t *)(base + o[7]);
-        w->mod = (float *)(base + o[8]);
     }
     return off;
 }
@@ -242,10 +242,13 @@ static aria_qgemm_epi epi_heads(int S, int H, int nsec, const int *kind, uint16_
     e.cos_t = dcos; e.sin_t = dsin; e.rot = rot; e.eps = eps;
     return e;
 }
-static aria_qgemm_epi epi_resid(int mode, int S, const float *gate, const float *add2) {
+/* gate = gate_t[col] + gate_g[b * g_bs + col] (gate_g may be NULL) */
+static aria_qgemm_epi epi_resid(int mode, int S, const float *gate_t, const float *gate_g, int g_bs,
+                                const float *add2) {
     aria_qgemm_epi e;
     memset(&e, 0, sizeof e);
-    e.mode = mode; e.rows_per_batch = S; e.gate = gate; e.add2 = add2;
+    e.mode = mode; e.rows_per_batch = S; e.gate = gate_t; e.gate_bs = 0; e.gate2 = gate_g; e.gate2_bs = g_bs;
+    e.add2 = add2;
     return e;
 }
 
@@ -304,16 +307,21 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
         return ARIA_HIP_EINVAL;
     }
     const int d = b->dim, H = b->H, M = B * S;
-    const size_t Bd = (size_t)B * d;
     const float eps_norm = 1e-5f, eps_qk = 1e-6f;
 
-    STEP(aria_k_mod_chunks(w.mod, b->tssg, dgcond, B, d, s), "k_mod_chunks");
-    const float *scale_self = w.mod, *shift_self = w.mod + Bd, *gate_self = w.mod + 2 * Bd;
-    const float *scale_ff = w.mod + 3 * Bd, *shift_ff = w.mod + 4 * Bd, *gate_ff = w.mod + 5 * Bd;
+    /* modulation chunk c (scale_self, shift_self, gate_self, scale_ff, shift_ff, gate_ff) =
+     * to_scale_shift_gate[c] + gcond[b][c] (src/aria_sa3_dit.c:152-156), formed where it is
+     * used: in the norm kernels and in the gated-residual epilogues */
+    const float *tc[6], *gc[6];
+    for (int c = 0; c < 6; c++) {
+        tc[c] = b->tssg + (size_t)c * d;
+        gc[c] = dgcond ? dgcond + (size_t)c * d : NULL;
+    }
+    const int gbs = 6 * d;
 
     /* ---- self-attention ---- */
-    STEP(aria_k_rownorm(w.h16, 1, dx, b->pre_norm, NULL, scale_self, shift_self, S, 0, 0, ARIA_NORM_RMS, M, d,
-                        eps_norm, s), "k_rownorm (pre_norm + adaLN)");
+    STEP(aria_k_rownorm_ada(w.h16, 1, dx, b->pre_norm, tc[0], tc[1], gc[0], gc[1], gbs, S, M, d, eps_norm, s),
+         "k_rownorm (pre_norm + adaLN)");
     {   /* qkv projection with q/k RMSNorm + RoPE and the head split in its epilogue */
         const int kind[3] = {0, 1, 2};
         uint16_t *dst[3] = {w.q16, w.k16, w.v16};
@@ -323,7 +331,7 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
     }
     STEP(aria_k_flash_attn(w.q16, w.k16, w.v16, w.att16, 1, B * H, H, S, S, s), "k_flash_attn (self)");
     {   /* x += (att . sa_to_out^T) * sigmoid(1 - gate_self) */
-        const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, gate_self, NULL);
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, tc[2], gc[2], gbs, NULL);
         STEP(gemm_e(&b->sa_out, dx, w.att16, NULL, M, &e, s), "k_qgemm (sa_to_out + gated residual)");
     }
 
@@ -339,12 +347,12 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
     }
     STEP(aria_k_flash_attn(w.q16, dk, dv, w.att16, 1, B * H, H, S, Sc, s), "k_flash_attn (cross)");
     {   /* x += att . ca_to_out^T, then the local-additive cond (src/aria_sa3_dit.c:242-252) */
-        const aria_qgemm_epi e = epi_resid(ARIA_EPI_ADD, S, NULL, dlocal);
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_ADD, S, NULL, NULL, 0, dlocal);
         STEP(gemm_e(&b->ca_out, dx, w.att16, NULL, M, &e, s), "k_qgemm (ca_to_out + residual)");
     }
 
     /* ---- feed-forward ---- */
-    STEP(aria_k_rownorm(w.h16, 1, dx, b->ff_norm, NULL, scale_ff, shift_ff, S, 0, 0, ARIA_NORM_RMS, M, d, eps_norm, s),
+    STEP(aria_k_rownorm_ada(w.h16, 1, dx, b->ff_norm, tc[3], tc[4], gc[3], gc[4], gbs, S, M, d, eps_norm, s),
          "k_rownorm (ff_norm + adaLN)");
     if (b->ffn == ARIA_FFN_GLU) {   /* g16 = silu(gate) * value in the projection's epilogue */
         aria_qgemm_epi e;
@@ -356,7 +364,7 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
         STEP(gemm(&b->ff_in, w.ff16, 1, w.h16, b->ff_in_b, M, 1, s), "k_qgemm (ff_in + GELU)");
     }
     {   /* x += (g16 . ff_out^T + b) * sigmoid(1 - gate_ff) */
-        const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, gate_ff, NULL);
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, tc[5], gc[5], gbs, NULL);
         STEP(gemm_e(&b->ff_out, dx, w.ff16, b->ff_out_b, M, &e, s), "k_qgemm (ff_out + gated residual)");
     }
     return 0;

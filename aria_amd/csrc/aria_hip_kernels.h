@@ -28,6 +28,12 @@ hipError_t aria_k_rownorm(void *y, int out_f16, const float *x, const float *w, 
                           const float *scale, const float *shift, int rows_per_batch,
                           int gelu, int resid, int norm, int rows, int dim, float eps,
                           hipStream_t s);
+/* RMSNorm + adaLN with scale = scale_t[c] + scale_g[b * g_bs + c] formed in place (scale_g,
+ * shift_g may be NULL); w may be NULL */
+hipError_t aria_k_rownorm_ada(void *y, int out_f16, const float *x, const float *w,
+                              const float *scale_t, const float *shift_t, const float *scale_g,
+                              const float *shift_g, int g_bs, int rows_per_batch, int rows,
+                              int dim, float eps, hipStream_t s);
 
 /* Elementwise (k_elementwise.hip). n counts floats. */
 hipError_t aria_k_add(float *y, const float *a, const float *b, size_t n, hipStream_t s);
@@ -87,7 +93,8 @@ hipError_t aria_k_q4_dequant(float *W, const uint8_t *q, const float *scale, int
 enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2 };
 /* Fused epilogues, applied to v = acc * scale (+ bias) (GELU'd when gelu != 0):
  *   STORE     y = v (fp32 or fp16)
- *   GATE_RES  y = y + v * sigmoid(1 - gate[row / rows_per_batch][col])   (fp32, in place)
+ *   GATE_RES  y = y + v * sigmoid(1 - g), g = gate[b * gate_bs + col]
+ *             (+ gate2[b * gate2_bs + col]), b = row / rows_per_batch      (fp32, in place)
  *   ADD       y = (y + v) (+ add2)                                        (fp32, in place)
  *   HEADS     the N columns are nsec sections of heads*64: each 64-column head is
  *             RMS-normalised (w, statistic in double) and rotated (RoPE rot dims) for
@@ -98,7 +105,8 @@ enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2 };
 enum { ARIA_EPI_STORE = 0, ARIA_EPI_GATE_RES = 1, ARIA_EPI_ADD = 2, ARIA_EPI_HEADS = 3, ARIA_EPI_GLU = 4 };
 typedef struct {
     int mode, rows_per_batch;
-    const float *gate, *add2;
+    const float *gate, *add2, *gate2;
+    int gate_bs, gate2_bs;
     int heads, nsec, kind[3];
     uint16_t *dst[3];
     const float *w[3];

@@ -27,6 +27,11 @@ enum { EPI_MOD = 1, EPI_GELU = 2, EPI_RES = 4, EPI_F16 = 8 };
 struct NormArgs {
     void *y;
     const float *x, *w, *b, *scale, *shift;
+    /* modulation = scale[bt * mod_bs + c] (+ scale_add[bt * add_bs + c]), shift likewise:
+     * the DiT passes the block's to_scale_shift_gate chunk (batch stride 0) plus the
+     * per-request gcond chunk, so the sum is formed here instead of in a separate pass */
+    const float *scale_add, *shift_add;
+    int mod_bs, add_bs;
     int rows_per_batch, rows, dim;
     float eps;
     int gelu, resid, f16;
@@ -75,6 +80,41 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
 #pragma unroll
     for (int j = 0; j < VPL; j++) v[j] = x4[j * LPR + l];
 
+    /* the broadcast vectors are loaded with the row, before the reduction, so their
+     * latency overlaps the row's instead of following it */
+    const float4 *w4 = reinterpret_cast<const float4 *>(a.w);
+    const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
+    const bool hw = a.w != nullptr, hb = a.b != nullptr;
+    float4 wv[VPL], bv[VPL], scv[VPL], shv[VPL];
+    {
+        const float4 *sc4 = nullptr, *sh4 = nullptr, *sca4 = nullptr, *sha4 = nullptr;
+        if (EPI & EPI_MOD) {
+            const int bt = row / a.rows_per_batch;
+            sc4 = reinterpret_cast<const float4 *>(a.scale + (size_t)bt * a.mod_bs);
+            sh4 = reinterpret_cast<const float4 *>(a.shift + (size_t)bt * a.mod_bs);
+            if (a.scale_add) {
+                sca4 = reinterpret_cast<const float4 *>(a.scale_add + (size_t)bt * a.add_bs);
+                sha4 = reinterpret_cast<const float4 *>(a.shift_add + (size_t)bt * a.add_bs);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+            const int c4 = j * LPR + l;
+            wv[j] = hw ? w4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            bv[j] = hb ? b4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            scv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            shv[j] = scv[j];
+            if (EPI & EPI_MOD) {
+                scv[j] = sc4[c4]; shv[j] = sh4[c4];
+                if (sca4) {
+                    const float4 sa = sca4[c4], ha = sha4[c4];
+                    scv[j] = make_float4(scv[j].x + sa.x, scv[j].y + sa.y, scv[j].z + sa.z, scv[j].w + sa.w);
+                    shv[j] = make_float4(shv[j].x + ha.x, shv[j].y + ha.y, shv[j].z + ha.z, shv[j].w + ha.w);
+                }
+            }
+        }
+    }
+
     float inv = 0.0f;
     double mu = 0.0, rstd = 0.0;
     if (NORM == ARIA_NORM_LAYER) {
@@ -104,27 +144,14 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
         inv = (float)(1.0 / sqrt(s / dim + (double)a.eps));
     }
 
-    const float4 *w4 = reinterpret_cast<const float4 *>(a.w);
-    const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
-    const float4 *sc4 = nullptr, *sh4 = nullptr;
-    if (EPI & EPI_MOD) {
-        const int bt = row / a.rows_per_batch;
-        sc4 = reinterpret_cast<const float4 *>(a.scale + (size_t)bt * dim);
-        sh4 = reinterpret_cast<const float4 *>(a.shift + (size_t)bt * dim);
-    }
-    const bool hw = a.w != nullptr, hb = a.b != nullptr;
 #pragma unroll
     for (int j = 0; j < VPL; j++) {
         const int c4 = j * LPR + l;
-        const float4 wv = hw ? w4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 bv = hb ? b4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        float4 scv = make_float4(0.f, 0.f, 0.f, 0.f), shv = scv;
-        if (EPI & EPI_MOD) { scv = sc4[c4]; shv = sh4[c4]; }
         float4 o;
-        o.x = epi_elem<EPI>(norm_elem<NORM>(v[j].x, inv, mu, rstd, hw, wv.x, hb, bv.x), v[j].x, scv.x, shv.x);
-        o.y = epi_elem<EPI>(norm_elem<NORM>(v[j].y, inv, mu, rstd, hw, wv.y, hb, bv.y), v[j].y, scv.y, shv.y);
-        o.z = epi_elem<EPI>(norm_elem<NORM>(v[j].z, inv, mu, rstd, hw, wv.z, hb, bv.z), v[j].z, scv.z, shv.z);
-        o.w = epi_elem<EPI>(norm_elem<NORM>(v[j].w, inv, mu, rstd, hw, wv.w, hb, bv.w), v[j].w, scv.w, shv.w);
+        o.x = epi_elem<EPI>(norm_elem<NORM>(v[j].x, inv, mu, rstd, hw, wv[j].x, hb, bv[j].x), v[j].x, scv[j].x, shv[j].x);
+        o.y = epi_elem<EPI>(norm_elem<NORM>(v[j].y, inv, mu, rstd, hw, wv[j].y, hb, bv[j].y), v[j].y, scv[j].y, shv[j].y);
+        o.z = epi_elem<EPI>(norm_elem<NORM>(v[j].z, inv, mu, rstd, hw, wv[j].z, hb, bv[j].z), v[j].z, scv[j].z, shv[j].z);
+        o.w = epi_elem<EPI>(norm_elem<NORM>(v[j].w, inv, mu, rstd, hw, wv[j].w, hb, bv[j].w), v[j].w, scv[j].w, shv[j].w);
         if (EPI & EPI_F16) {
             uint2 p;
             p.x = (uint32_t)f2h_bits(o.x) | ((uint32_t)f2h_bits(o.y) << 16);
@@ -162,16 +189,24 @@ __global__ __launch_bounds__(256) void k_rownorm_g(NormArgs a) {
         inv = (float)(1.0 / sqrt(s / dim + (double)a.eps));
     }
     const float *sc = nullptr, *sh = nullptr;
+    const float *sca = nullptr, *sha = nullptr;
     if (a.scale) {
         int bt = row / a.rows_per_batch;
-        sc = a.scale + (size_t)bt * dim;
-        sh = a.shift + (size_t)bt * dim;
+        sc = a.scale + (size_t)bt * a.mod_bs;
+        sh = a.shift + (size_t)bt * a.mod_bs;
+        if (a.scale_add) {
+            sca = a.scale_add + (size_t)bt * a.add_bs;
+            sha = a.shift_add + (size_t)bt * a.add_bs;
+        }
     }
     const bool hw = a.w != nullptr, hb = a.b != nullptr;
     for (int c = lane; c < dim; c += 64) {
         float xv = xr[c];
         float n = norm_elem<NORM>(xv, inv, mu, rstd, hw, hw ? a.w[c] : 0.0f, hb, hb ? a.b[c] : 0.0f);
-        if (sc) { float t = 1.0f + sc[c]; n = n * t; n = n + sh[c]; }
+        if (sc) {
+            const float scv = sca ? sc[c] + sca[c] : sc[c], shv = sha ? sh[c] + sha[c] : sh[c];
+            float t = 1.0f + scv; n = n * t; n = n + shv;
+        }
         if (a.gelu) n = gelu_tanh_f(n);
         if (a.resid) n = n + xv;
         if (a.f16) ((uint16_t *)a.y)[(size_t)row * dim + c] = f2h_bits(n);
@@ -203,7 +238,8 @@ static hipError_t launch_norm(const NormArgs &a, hipStream_t s) {
     const int dim = a.dim;
     const bool vec = (dim % 4 == 0) && al16(a.x) && (a.f16 ? ((uintptr_t)a.y & 7u) == 0 : al16(a.y)) &&
                      (!a.w || al16(a.w)) && (!a.b || al16(a.b)) && (!a.scale || al16(a.scale)) &&
-                     (!a.shift || al16(a.shift));
+                     (!a.shift || al16(a.shift)) && (!a.scale_add || al16(a.scale_add)) &&
+                     (!a.shift_add || al16(a.shift_add)) && a.mod_bs % 4 == 0 && a.add_bs % 4 == 0;
     int epi = (a.scale ? EPI_MOD : 0) | (a.gelu ? EPI_GELU : 0) | (a.resid ? EPI_RES : 0) | (a.f16 ? EPI_F16 : 0);
     /* only these epilogues are instantiated for the register path; others take the generic kernel */
     const bool known = epi == 0 || epi == EPI_F16 || epi == EPI_MOD || epi == (EPI_MOD | EPI_F16) ||
@@ -232,6 +268,7 @@ extern "C" hipError_t aria_k_rownorm(void *y, int out_f16, const float *x, const
     if (rows <= 0 || dim <= 0) return hipSuccess;
     NormArgs a;
     a.y = y; a.x = x; a.w = w; a.b = b; a.scale = scale; a.shift = shift;
+    a.scale_add = nullptr; a.shift_add = nullptr; a.mod_bs = dim; a.add_bs = 0;
     a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows;
     a.rows = rows; a.dim = dim; a.eps = eps;
     a.gelu = gelu; a.resid = resid; a.f16 = out_f16;
@@ -240,4 +277,22 @@ extern "C" hipError_t aria_k_rownorm(void *y, int out_f16, const float *x, const
         case ARIA_NORM_LAYER: return launch_norm<ARIA_NORM_LAYER>(a, s);
         default: return launch_norm<ARIA_NORM_RMS>(a, s);
     }
+}
+
+/* RMSNorm + adaLN modulate with the modulation formed in place: scale = scale_t[c] +
+ * scale_g[b * g_bs + c] (scale_g NULL: scale_t alone), shift likewise; the result in fp16
+ * or fp32. The DiT passes its to_scale_shift_gate chunks (scale_t, shift_t) and the
+ * request's gcond chunks (batch stride 6 * dim). */
+extern "C" hipError_t aria_k_rownorm_ada(void *y, int out_f16, const float *x, const float *w,
+                                         const float *scale_t, const float *shift_t, const float *scale_g,
+                                         const float *shift_g, int g_bs, int rows_per_batch, int rows,
+                                         int dim, float eps, hipStream_t s) {
+    if (rows <= 0 || dim <= 0) return hipSuccess;
+    NormArgs a;
+    a.y = y; a.x = x; a.w = w; a.b = nullptr; a.scale = scale_t; a.shift = shift_t;
+    a.scale_add = scale_g; a.shift_add = shift_g; a.mod_bs = 0; a.add_bs = g_bs;
+    a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows;
+    a.rows = rows; a.dim = dim; a.eps = eps;
+    a.gelu = 0; a.resid = 0; a.f16 = out_f16;
+    return launch_norm<ARIA_NORM_RMS>(a, s);
 }

@@ -99,6 +99,32 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
         if (WT == ARIA_WQ8) sc = *reinterpret_cast<const float4 *>(a.scale + nb);
         if (a.bias) bb = *reinterpret_cast<const float4 *>(a.bias + nb);
     }
+    /* GATE_RES: the gate depends on (batch, column) only, so sigmoid(1 - gate) is formed
+     * once per lane for the (at most two) batches this wave's rows span; a tile spanning
+     * more batches (sequences shorter than the tile) reads it per row */
+    auto gate_at = [&](int bt, int col) -> float4 {
+        float4 g = *reinterpret_cast<const float4 *>(a.epi.gate + (size_t)bt * a.epi.gate_bs + col);
+        if (a.epi.gate2) {   /* the gate formed in place: chunk of to_scale_shift_gate + gcond */
+            const float4 ga = *reinterpret_cast<const float4 *>(a.epi.gate2 + (size_t)bt * a.epi.gate2_bs + col);
+            g = make_float4(g.x + ga.x, g.y + ga.y, g.z + ga.z, g.w + ga.w);
+        }
+        return g;
+    };
+    bool gpre = false;
+    int blo = 0;
+    float4 gs0 = make_float4(0.f, 0.f, 0.f, 0.f), gs1 = gs0;
+    if constexpr (MODE == ARIA_EPI_GATE_RES) {
+        const int rpb = a.epi.rows_per_batch;
+        const int mlast = min(mw + 32 * FM - 1, a.M - 1);
+        blo = min(mw, a.M - 1) / rpb;
+        gpre = mlast / rpb <= blo + 1;
+        if (gpre) {
+            const int nbc = col_ok ? nb : 0, bhi = min(blo + 1, (a.M - 1) / rpb);
+            const float4 g0 = gate_at(blo, nbc), g1 = gate_at(bhi, nbc);
+            gs0 = make_float4(gate_sig_f(g0.x), gate_sig_f(g0.y), gate_sig_f(g0.z), gate_sig_f(g0.w));
+            gs1 = make_float4(gate_sig_f(g1.x), gate_sig_f(g1.y), gate_sig_f(g1.z), gate_sig_f(g1.w));
+        }
+    }
     /* HEADS: per-lane constants of the epilogue (section, head, norm gains, RoPE lanes) */
     const aria_qgemm_epi &e = a.epi;
     int hh = 0, l16 = 0, kind = 2, rh = 0, i0 = 0;
@@ -177,9 +203,8 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
             for (int it = 0; it < NIT; it++) {
                 const int mc = min(mrow[it], a.M - 1);
                 rr[it] = *reinterpret_cast<const float4 *>((const float *)a.y + (size_t)mc * a.N + nbc);
-                if (MODE == ARIA_EPI_GATE_RES)
-                    g2[it] = *reinterpret_cast<const float4 *>(e.gate + (size_t)(mc / e.rows_per_batch) * a.N + nbc);
-                else if (e.add2)
+                if (MODE == ARIA_EPI_GATE_RES && !gpre) g2[it] = gate_at(mc / e.rows_per_batch, nbc);
+                else if (MODE == ARIA_EPI_ADD && e.add2)
                     g2[it] = *reinterpret_cast<const float4 *>(e.add2 + (size_t)mc * a.N + nbc);
             }
 #pragma unroll
@@ -189,8 +214,11 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
                 float4 o;
                 if (MODE == ARIA_EPI_GATE_RES) {
                     /* y += v * sigmoid(1 - gate): the rounding order of k_gate_residual */
-                    o = make_float4(rr[it].x + v[it][0] * gate_sig_f(g2[it].x), rr[it].y + v[it][1] * gate_sig_f(g2[it].y),
-                                    rr[it].z + v[it][2] * gate_sig_f(g2[it].z), rr[it].w + v[it][3] * gate_sig_f(g2[it].w));
+                    float4 sg;
+                    if (gpre) sg = (m / e.rows_per_batch == blo) ? gs0 : gs1;
+                    else sg = make_float4(gate_sig_f(g2[it].x), gate_sig_f(g2[it].y), gate_sig_f(g2[it].z), gate_sig_f(g2[it].w));
+                    o = make_float4(rr[it].x + v[it][0] * sg.x, rr[it].y + v[it][1] * sg.y,
+                                    rr[it].z + v[it][2] * sg.z, rr[it].w + v[it][3] * sg.w);
                 } else {
                     o = make_float4(rr[it].x + v[it][0], rr[it].y + v[it][1], rr[it].z + v[it][2], rr[it].w + v[it][3]);
                     if (e.add2) o = make_float4(o.x + g2[it].x, o.y + g2[it].y, o.z + g2[it].z, o.w + g2[it].w);
