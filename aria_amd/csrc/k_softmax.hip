@@ -28,20 +28,28 @@ __global__ __launch_bounds__(256) void k_softmax_v(float *x, int rows, int cols,
     const int n4 = cols >> 2;
     float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * cols);
     const float4 *mr = mask ? reinterpret_cast<const float4 *>(mask + (size_t)row * cols) : nullptr;
+    /* every load of the row is issued before any is used: folding the max into the
+     * guarded load loop made each load wait for the previous one (~12% slower) */
     float4 v[NV];
-    float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
         const int idx = j * 64 + lane;
-        if (idx < n4) {
-            v[j] = ld_nt(xr + idx);
-            if (mr) {
-                float4 k = mr[idx];
+        v[j] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (idx < n4) v[j] = ld_nt(xr + idx);
+    }
+    if (mr) {
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const int idx = j * 64 + lane;
+            if (idx < n4) {
+                const float4 k = mr[idx];
                 v[j].x += k.x; v[j].y += k.y; v[j].z += k.z; v[j].w += k.w;
             }
-            m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
         }
     }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NV; j++) m = fmaxf(fmaxf(m, v[j].x), fmaxf(v[j].y, fmaxf(v[j].z, v[j].w)));
     m = grp_max<64>(m);
     float s = 0.0f;
 #pragma unroll
