@@ -165,11 +165,20 @@ __device__ __forceinline__ uint32_t pack2h_rn(float x, float y) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_v));
 }
 
-__global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * 64];
-    __shared__ __attribute__((aligned(16))) uint16_t Vs[2][KT * 64];
+/* KS = 1: 4 waves, all keys. KS = 2: 8 waves; waves 4-7 take the second half of the key
+ * tiles with their own LDS buffers, and the halves merge (max, row sum, O) through LDS at
+ * the end: twice the waves per query block without any exchange between workgroups. Both
+ * halves run the same number of loop trips, so every barrier is reached by all waves. */
+template <int KS>
+__global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) void k_flash_attn(AttnArgs a) {
+    /* one buffer: K tiles [half][buf], then V tiles [half][buf], each KT x 64 fp16; after
+     * the key loop it holds the merge exchange (4 waves x 34 x 64 floats = 34.8 KB) */
+    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * KS * 2 * KT * 64];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+    const int half = KS == 1 ? 0 : (int)(threadIdx.x >> 8);
+    uint16_t *const Kb0 = smem + (half * 2) * (KT * 64), *const Kb1 = Kb0 + KT * 64;
+    uint16_t *const Vb0 = smem + (KS * 2 + half * 2) * (KT * 64), *const Vb1 = Vb0 + KT * 64;
+    const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
     const int bh = blockIdx.y;
     const int q0 = blockIdx.x * 128 + wave * 32;
     const uint16_t *Qh = a.q + (size_t)bh * a.Nq * 64;
@@ -198,35 +207,34 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
         rv1 = *reinterpret_cast<const uint4 *>(Vh + off1);
     };
     auto sstore = [&](int buf) {
-        *reinterpret_cast<uint4 *>(&Ks[buf][k_off(sl0 >> 3, sl0 & 7)]) = rk0;
-        *reinterpret_cast<uint4 *>(&Vs[buf][v_off(sl0 >> 3, 8 * (sl0 & 7))]) = rv0;
-        *reinterpret_cast<uint4 *>(&Ks[buf][k_off(sl1 >> 3, sl1 & 7)]) = rk1;
-        *reinterpret_cast<uint4 *>(&Vs[buf][v_off(sl1 >> 3, 8 * (sl1 & 7))]) = rv1;
+        uint16_t *Kd = buf ? Kb1 : Kb0, *Vd = buf ? Vb1 : Vb0;
+        *reinterpret_cast<uint4 *>(&Kd[k_off(sl0 >> 3, sl0 & 7)]) = rk0;
+        *reinterpret_cast<uint4 *>(&Vd[v_off(sl0 >> 3, 8 * (sl0 & 7))]) = rv0;
+        *reinterpret_cast<uint4 *>(&Kd[k_off(sl1 >> 3, sl1 & 7)]) = rk1;
+        *reinterpret_cast<uint4 *>(&Vd[v_off(sl1 >> 3, 8 * (sl1 & 7))]) = rv1;
     };
 
-    f32x16_t oacc[2], lacc;
+    f32x16_t oacc[2];
 #pragma unroll
-    for (int r = 0; r < 16; r++) { oacc[0][r] = 0.0f; oacc[1][r] = 0.0f; lacc[r] = 0.0f; }
-    const half8_t ones = {(_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f,
-                          (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f, (_Float16)1.0f};
+    for (int r = 0; r < 16; r++) { oacc[0][r] = 0.0f; oacc[1][r] = 0.0f; }
+    /* this lane's share of the row sum l (its 32 keys of each tile; the partner lane l^32
+     * holds the other 32), accumulated from the same fp16 P that multiplies V */
+    float lsum = 0.0f;
+    typedef _Float16 half2_v __attribute__((ext_vector_type(2)));
+    const half2_v one2 = {(_Float16)1.0f, (_Float16)1.0f};
     float m_use = -INFINITY;   /* running reference max, scaled (log2) units */
 
-    /* per-lane LDS offsets (halves) of every fragment read, hoisted out of the key loop */
-    int koff[2][4], voff[4][2][2];
+    /* per-lane LDS offsets (halves) of the fragment reads, hoisted out of the key loop. The
+     * swizzles depend only on lane bits: K block kb (keys 32kb..) sits 32*64*kb further, V key
+     * step s16 (keys 16 s16..) 16*64*s16 further and its second 8 keys 8*64 further, all
+     * immediates, so six base offsets cover every read */
+    int koff[4], voff[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int ds = 0; ds < 4; ds++) koff[kb][ds] = k_off(32 * kb + l32, 2 * ds + g);
+    for (int ds = 0; ds < 4; ds++) koff[ds] = k_off(l32, 2 * ds + g);
     {
         const int v = (lane & 15) >> 2, w = lane & 3, G = lane >> 4;
 #pragma unroll
-        for (int s16 = 0; s16 < 4; s16++)
-#pragma unroll
-            for (int dt = 0; dt < 2; dt++) {
-                const int key = 16 * s16 + 4 * (G >> 1) + v, d0 = 32 * dt + 16 * (G & 1) + 4 * w;
-                voff[s16][dt][0] = v_off(key, d0);
-                voff[s16][dt][1] = v_off(key + 8, d0);
-            }
+        for (int dt = 0; dt < 2; dt++) voff[dt] = v_off(4 * (G >> 1) + v, 32 * dt + 16 * (G & 1) + 4 * w);
     }
 
     /* one 64-key tile from LDS buffer BUF (a compile-time constant, so every LDS offset
@@ -240,7 +248,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
             for (int r = 0; r < 16; r++) sc[kb][r] = 0.0f;
 #pragma unroll
             for (int ds = 0; ds < 4; ds++)
-                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ld_h8(K + koff[kb][ds]), qf[ds], sc[kb], 0, 0, 0);
+                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ld_h8(K + koff[ds] + 32 * 64 * kb), qf[ds], sc[kb], 0, 0, 0);
         }
         if (kt0 + KT > a.Nk) {   /* ragged last tile: keys past the end get -inf */
 #pragma unroll
@@ -264,7 +272,8 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
             const float m_new = fmaxf(m_use, mt);
             const float alpha = __builtin_amdgcn_exp2f(m_use - m_new);
 #pragma unroll
-            for (int r = 0; r < 16; r++) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; lacc[r] *= alpha; }
+            for (int r = 0; r < 16; r++) { oacc[0][r] *= alpha; oacc[1][r] *= alpha; }
+            lsum *= alpha;
             m_use = m_new;
         }
         /* P^T = exp2(s * scale - m) in fp16; MFMA step ks of block kb takes accumulator
@@ -282,41 +291,76 @@ __global__ __launch_bounds__(256) void k_flash_attn(AttnArgs a) {
                 const int s16 = 2 * kb + ks;
 #pragma unroll
                 for (int dt = 0; dt < 2; dt++) {
-                    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[s16][dt][0]));
-                    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[s16][dt][1]));
+                    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[dt] + 16 * 64 * s16));
+                    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[dt] + 16 * 64 * s16 + 8 * 64));
                     const half4_t hl = __builtin_bit_cast(half4_t, lo), hh = __builtin_bit_cast(half4_t, hi);
                     const half8_t vf = {hl[0], hl[1], hl[2], hl[3], hh[0], hh[1], hh[2], hh[3]};
                     oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, oacc[dt], 0, 0, 0);
                 }
-                /* row sums of the rounded P on the matrix core: every row of lacc = sum_k P */
-                lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pf, lacc, 0, 0, 0);
+                /* row sum of the rounded P: exact fp16 products, fp32 accumulation */
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_v, __builtin_bit_cast(uint4, pf)[e]), one2, lsum, false);
             }
         }
     };
 
-    const int ntiles = (a.Nk + KT - 1) / KT;
-    gload(0);
-    sstore(0);
+    /* this half's key tiles [tb, tb + nt); niter = trips every half runs */
+    const int ntiles_all = (a.Nk + KT - 1) / KT;
+    const int niter = (ntiles_all + KS - 1) / KS;
+    const int tb = half * niter;
+    const int nt = max(0, min(niter, ntiles_all - tb));
+    const int kbase = tb * KT;
+    const uint16_t *K0 = Kb0, *V0 = Vb0, *K1 = Kb1, *V1 = Vb1;
+    if (nt > 0) {
+        gload(kbase);
+        sstore(0);
+    }
     __syncthreads();
     /* two tiles per trip so each LDS buffer is a fixed address; buffer b^1 was last read
      * one tile earlier, before that tile's closing barrier */
-    for (int t = 0; t < ntiles; t += 2) {
-        if (t + 1 < ntiles) gload((t + 1) * KT);
-        tile(t * KT, Ks[0], Vs[0]);
-        if (t + 1 < ntiles) sstore(1);
+    for (int t = 0; t < niter; t += 2) {
+        if (t + 1 < nt) gload(kbase + (t + 1) * KT);
+        if (t < nt) tile(kbase + t * KT, K0, V0);
+        if (t + 1 < nt) sstore(1);
         __syncthreads();
-        if (t + 1 < ntiles) {
-            if (t + 2 < ntiles) gload((t + 2) * KT);
-            tile((t + 1) * KT, Ks[1], Vs[1]);
-            if (t + 2 < ntiles) sstore(0);
+        if (t + 1 < niter) {
+            if (t + 2 < nt) gload(kbase + (t + 2) * KT);
+            if (t + 1 < nt) tile(kbase + (t + 1) * KT, K1, V1);
+            if (t + 2 < nt) sstore(0);
             __syncthreads();
         }
+    }
+
+    float lrow = lsum + __shfl_xor(lsum, 32, ARIA_WAVE);   /* the query's full row sum */
+
+    if constexpr (KS == 2) {
+        /* merge: the second half hands (O, l, m) to the first through LDS (the tile buffers
+         * are free after the last trip's barrier); per wave 64 lanes x 34 floats */
+        float *X = reinterpret_cast<float *>(smem) + wave * 34 * 64 + lane;
+        if (half == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) { X[r * 64] = oacc[0][r]; X[(16 + r) * 64] = oacc[1][r]; }
+            X[32 * 64] = lrow;
+            X[33 * 64] = m_use;
+        }
+        __syncthreads();
+        if (half == 1) return;
+        const float m1 = X[33 * 64], l1 = X[32 * 64];
+        const float m = fmaxf(m_use, m1);   /* half 0 always has keys: m is finite */
+        const float a0 = __builtin_amdgcn_exp2f(m_use - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            oacc[0][r] = oacc[0][r] * a0 + X[r * 64] * a1;
+            oacc[1][r] = oacc[1][r] * a0 + X[(16 + r) * 64] * a1;
+        }
+        lrow = lrow * a0 + l1 * a1;
     }
 
     /* O[q, d] = O^T[d, q] / l ; lane holds query q0 + l32, d = 32dt + 8(r/4) + 4g + r%4 */
     const int qi = q0 + l32;
     if (qi >= a.Nq) return;
-    const float inv = 1.0f / lacc[0];
+    const float inv = 1.0f / lrow;
     const int b = bh / a.H, h = bh % a.H;
     const size_t orow = ((size_t)b * a.Nq + qi) * (size_t)(a.H * 64) + h * 64;
 #pragma unroll
@@ -344,6 +388,11 @@ extern "C" hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, co
     a.q = q; a.k = k; a.v = v; a.o = o; a.H = H; a.Nq = Nq; a.Nk = Nk; a.o_f16 = o_f16;
     a.scale_log2 = 0.125f * ARIA_LOG2E;
     dim3 grid((Nq + 127) / 128, BH);
-    hipLaunchKernelGGL(k_flash_attn, grid, dim3(256), 0, s, a);
+    /* split the keys inside the workgroup when there are enough tiles for both halves
+     * (S = 1296 self-attention: 21 tiles); short key sets (the 256 cross keys) run 4 waves */
+    if ((Nk + KT - 1) / KT >= 8)
+        hipLaunchKernelGGL(k_flash_attn<2>, grid, dim3(512), 0, s, a);
+    else
+        hipLaunchKernelGGL(k_flash_attn<1>, grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
