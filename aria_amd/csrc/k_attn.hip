@@ -21,12 +21,13 @@
  * softmax statistics need a single xor-32 exchange.
  *
  * Precision: Q, K, V and P are fp16, accumulation fp32, exp via v_exp_f32. The row sum
- * l is accumulated on the matrix core from the same fp16 P that multiplies V. The
- * running max is a lazy reference (moved only when a tile exceeds it by 2^8), so the
- * accumulators are rarely rescaled; O / l does not depend on the reference chosen.
- * Workgroup: 4 waves x 32 queries = 128 queries of one (batch, head); K and V tiles of
- * 64 keys are staged key-major in LDS (swizzled, conflict-free) with register prefetch
- * of the next tile; the V^T operand is read with the gfx950 transpose load
+ * l is accumulated (v_dot2_f32_f16, exact products) from the same fp16 P that multiplies
+ * V. The running max is a lazy reference (moved only when a tile exceeds it by 2^8), so
+ * the accumulators are rarely rescaled; O / l does not depend on the reference chosen.
+ * Workgroup: 4 waves x 32 queries = 128 queries of one (batch, head), or 8 waves when
+ * the keys are split in two halves inside the workgroup (long key sets); K and V tiles
+ * of 64 keys are staged key-major in LDS (swizzled, conflict-free) with register
+ * prefetch of the next tile; the V^T operand is read with the gfx950 transpose load
  * (ds_read_b64_tr_b16).
  */
 #include "aria_dev.h"
