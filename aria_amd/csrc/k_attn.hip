@@ -158,6 +158,13 @@ __device__ __forceinline__ int v_off(int key, int d) {
  * the 8 B rows addressed by lanes 4v+w (v = 0..3): addressing key kb' + v at d0 + 4w
  * delivers V[kb'+0..3][d0 + (lane & 15)] to each lane (voff below). */
 
+/* max(a, b, c) in one v_max3_f32 */
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 /* fp32 pair -> packed fp16, round to nearest even */
 __device__ __forceinline__ uint32_t pack2h_rn(float x, float y) {
     typedef float float2_v __attribute__((ext_vector_type(2)));
@@ -258,18 +265,23 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
                 for (int r = 0; r < 16; r++)
                     if (kt0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3) >= a.Nk) sc[kb][r] = -INFINITY;
         }
-        /* tile max over this lane's 32 keys and the partner lane's 32 */
-        float m3[8];
+        /* tile max over this lane's 32 keys and the partner lane's 32: a tree of 3-input
+         * maxima (15 v_max3_f32, depth 3; two-input fmaxf trees compile to twice as many ops) */
+        float t1[11];
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            m3[i] = fmaxf(fmaxf(sc[i >> 2][4 * (i & 3)], sc[i >> 2][4 * (i & 3) + 1]),
-                          fmaxf(sc[i >> 2][4 * (i & 3) + 2], sc[i >> 2][4 * (i & 3) + 3]));
-        float mt = fmaxf(fmaxf(fmaxf(m3[0], m3[1]), fmaxf(m3[2], m3[3])), fmaxf(fmaxf(m3[4], m3[5]), fmaxf(m3[6], m3[7])));
+        for (int i = 0; i < 10; i++) t1[i] = max3f(sc[(3 * i) >> 4][(3 * i) & 15], sc[(3 * i + 1) >> 4][(3 * i + 1) & 15],
+                                                   sc[(3 * i + 2) >> 4][(3 * i + 2) & 15]);
+        t1[10] = fmaxf(sc[1][14], sc[1][15]);
+        float mt = max3f(max3f(t1[0], t1[1], t1[2]), max3f(t1[3], t1[4], t1[5]), max3f(t1[6], t1[7], t1[8]));
+        mt = max3f(mt, t1[9], t1[10]);
         mt = fmaxf(mt, __shfl_xor(mt, 32, ARIA_WAVE)) * a.scale_log2;
         /* lazy rescale: the reference max only moves when the tile max exceeds it by more
          * than RESCALE_SLACK (probabilities stay <= 2^8, exact in fp16's range); the final
          * O / l is unchanged by the choice of reference */
         if (__ballot(mt > m_use + RESCALE_SLACK)) {
+            /* a real branch: without the marker the compiler predicates the 33 multiplies
+             * and runs them on every tile */
+            asm volatile("" ::: "memory");
             const float m_new = fmaxf(m_use, mt);
             const float alpha = __builtin_amdgcn_exp2f(m_use - m_new);
 #pragma unroll
