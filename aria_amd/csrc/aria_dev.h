@@ -96,6 +96,16 @@ __device__ __forceinline__ float tanh_fast(float u) {
     return 1.0f - 2.0f * rcp_fast(1.0f + e);
 }
 
+/* ---- rotate-half RoPE partner within a 16-lane group holding one 64-wide head ----
+ * Lane l holds dims 4l..4l+3; dim d < rh pairs with d + rh (rh = rot/2), so lane l < lp
+ * (lp = rh/4) pairs with lane l + lp and lane l in [lp, 2lp) with lane l - lp (lanes past
+ * 2lp hold unrotated dims; their partner value is unused). One ds_bpermute per value:
+ * DPP row shifts need a compile-time shift and were slower here. */
+__device__ __forceinline__ float rope_partner(float v, int lane, int lp) {
+    const int l16 = lane & 15;
+    return __shfl(v, (lane & 48) | (l16 < lp ? l16 + lp : l16 - lp), ARIA_WAVE);
+}
+
 /* ---- reference formulas, evaluation order as written in the reference C ---- */
 
 /* tanh GELU, src/aria_cpu.c:742-749: inner = c*(v + ((0.044715*v)*v)*v);

@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void k_qkv_prep(PrepArgs a) {
             const int rh = a.rot >> 1, lp = rh >> 2;   /* partner lane offset */
             float p[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) p[e] = __shfl(o[e], (lane & 48) | (l ^ lp), ARIA_WAVE);
+            for (int e = 0; e < 4; e++) p[e] = rope_partner(o[e], lane, lp);
             const int d0 = 4 * l;
             if (d0 < a.rot) {
                 const bool first = d0 < rh;

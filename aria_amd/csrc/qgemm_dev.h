@@ -251,7 +251,7 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
                         const int lp = rh >> 2;   /* partner lane offset */
                         float p[4];
 #pragma unroll
-                        for (int q = 0; q < 4; q++) p[q] = __shfl(w4[q], (lane & 48) | (l16 ^ lp), ARIA_WAVE);
+                        for (int q = 0; q < 4; q++) p[q] = rope_partner(w4[q], lane, lp);
                         if (rope) {
                             const float cv[4] = {cs[it].x, cs[it].y, cs[it].z, cs[it].w};
                             const float sv[4] = {sn[it].x, sn[it].y, sn[it].z, sn[it].w};
