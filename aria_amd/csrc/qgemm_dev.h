@@ -70,7 +70,7 @@ __device__ __forceinline__ int xcd_tile(int g, int T) {
  * loads and stores retire in order, so a load issued after a store would make the next
  * wait cover that store's whole write latency.
  * HEADS: the 16 lanes of a 64-column head share a row m (the wave's column range is
- * head-aligned); the arithmetic is k_qkv_prep's (k_attn.hip): RMS statistic in double
+ * head-aligned); the arithmetic is k_qkv_prep's (k_attn.hip): RMS statistic in fp32
  * over the head, (x * inv) * w, then rotate-half RoPE over the first rot dims. */
 #define EPI_ANY (-1)
 template <int FM, int FN, int WT, int MODE>
@@ -241,9 +241,9 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
                 const int m = mrow[it];
                 float *w4 = v[it];
                 if (kind != 2) {
-                    double ss = ((double)w4[0] * w4[0] + (double)w4[1] * w4[1]) + ((double)w4[2] * w4[2] + (double)w4[3] * w4[3]);
+                    float ss = (w4[0] * w4[0] + w4[1] * w4[1]) + (w4[2] * w4[2] + w4[3] * w4[3]);
                     ss = grp_sum<16>(ss);
-                    const float inv = (float)(1.0 / sqrt(ss / 64 + (double)e.eps));
+                    const float inv = __builtin_amdgcn_rsqf(ss * (1.0f / 64) + e.eps);
                     const float gv[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
                     for (int q = 0; q < 4; q++) w4[q] = (w4[q] * inv) * gv[q];   /* gv = 1 without gains */
