@@ -402,7 +402,8 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
     if constexpr (WT != ARIA_WF16) {
         /* weights-in-registers kernel: explicit tiles 9..12 (BM = 32 * (tiles - 8)), or the pick */
         const int fm = (tiles > NCFG) ? tiles - NCFG : (tiles == 0 ? pick_wr(a.M, a.N, a.K) : 0);
-        if (fm > 0 && a.K % 64 == 0) return qgemm_wr_launch(a, WT, fm, s);
+        const bool wr_ok = a.K % 64 == 0 && (!a.gelu || a.epi.mode == ARIA_EPI_STORE);
+        if (fm > 0 && wr_ok) return qgemm_wr_launch(a, WT, fm, s);
     }
     int c = (tiles >= 1 && tiles <= NCFG) ? tiles - 1 : pick_tiles(a.M, a.N, a.epi.mode == ARIA_EPI_HEADS);
     if (a.epi.mode == ARIA_EPI_HEADS && cfg_fn[c] < 2) c = pick_tiles(a.M, a.N, true);

@@ -91,7 +91,7 @@ __device__ __forceinline__ half8_t wr_frag(const WRegs<WT> &s, int j, int ks, ui
     return __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-template <int WT, int FM, int MINB, int MODE>
+template <int WT, int FM, int MINB, int MODE, bool GELU>
 __global__ __launch_bounds__(256, MINB) void k_qgemm_wr(QArgs a, int NTN, int T) {
     constexpr int FN = 2, BM = 32 * FM, BN = 256;
     constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
@@ -221,18 +221,20 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_wr(QArgs a, int NTN, int T)
     }
 
     float *E = reinterpret_cast<float *>(lds) + wave * (32 * EPI_STRIDE / 4);
-    epilogue<FM, FN, WT, MODE>(a, acc, E, lane, m0, n0 + wave * 64);
+    epilogue<FM, FN, WT, MODE, GELU>(a, acc, E, lane, m0, n0 + wave * 64);
 }
 
-template <int WT, int FM, int MODE>
+template <int WT, int FM, int MODE, bool GELU = false>
 static void launch_wr_m(const QArgs &a, hipStream_t s) {
     constexpr int BM = 32 * FM, BN = 256;
     const int MT = (a.M + BM - 1) / BM, NTN = (a.N + BN - 1) / BN, T = MT * NTN;
     const int grid = ((T + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_qgemm_wr<WT, FM, (FM <= 2 ? 2 : 1), MODE>), dim3(grid), dim3(256), 0, s, a, NTN, T);
+    hipLaunchKernelGGL((k_qgemm_wr<WT, FM, (FM <= 2 ? 2 : 1), MODE, GELU>), dim3(grid), dim3(256), 0, s, a, NTN, T);
 }
 /* one kernel per fused epilogue mode: a run-time mode switch inside the store loop
- * makes every store wait for the loads of the modes that read */
+ * makes every store wait for the loads of the modes that read. GELU is compiled in for
+ * the plain store only (the FFN input projection); the caller sends GELU with another
+ * mode to the LDS-operand kernel. */
 template <int WT, int FM>
 static void launch_wr(const QArgs &a, hipStream_t s) {
     switch (a.epi.mode) {
@@ -240,7 +242,10 @@ static void launch_wr(const QArgs &a, hipStream_t s) {
         case ARIA_EPI_ADD: launch_wr_m<WT, FM, ARIA_EPI_ADD>(a, s); break;
         case ARIA_EPI_HEADS: launch_wr_m<WT, FM, ARIA_EPI_HEADS>(a, s); break;
         case ARIA_EPI_GLU: launch_wr_m<WT, FM, ARIA_EPI_GLU>(a, s); break;
-        default: launch_wr_m<WT, FM, ARIA_EPI_STORE>(a, s); break;
+        default:
+            if (a.gelu) launch_wr_m<WT, FM, ARIA_EPI_STORE, true>(a, s);
+            else launch_wr_m<WT, FM, ARIA_EPI_STORE>(a, s);
+            break;
     }
 }
 

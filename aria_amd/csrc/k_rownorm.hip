@@ -12,17 +12,27 @@
  * no barrier) and writes the transformed row once: HBM traffic = read x + write y.
  * Broadcast vectors (w, b, scale, shift) are read as float4 at the same column.
  *
- * Statistics follow the reference: sum of squares accumulated in double
+ * RMS statistics follow the reference: sum of squares accumulated in double
  * (src/aria_cpu.c:57-98), inv = (float)(1.0/sqrt(ss/dim + eps)), then the
- * per-element products in float with separate roundings. LayerNorm (which has
- * no reference op) keeps mean, variance and (x-mean)*rstd in double.
+ * per-element products in float with separate roundings, so the output matches
+ * the reference nearly bit for bit. LayerNorm (which has no reference op) is two
+ * fp32 passes over the registers: mean = sum/dim, then the centred sum of squares
+ * (fma), rstd = v_rsq_f32(var + eps), y = (x - mean)*rstd. Against a double
+ * statistic this differs by ~1e-7 relative; the double form cost ~10 VALU per
+ * element (conversions, fp64 DPP reductions, divide and sqrt), which at 2.5 waves
+ * per SIMD is about 0.6 us of issue time per launch at [2592, 1024].
  *
- * The epilogue is a compile-time mask (EPI): modulate, GELU, residual, half output.
+ * The register path is compiled per operand set (EPI mask): gain, bias, modulate,
+ * second modulation term, GELU, residual, half output. With these as run-time
+ * flags the optional operands cost a select and a zero fill per element (~110 of
+ * the fused chain's VALU); launch_norm instantiates the combinations the callers
+ * use and sends any other to the generic kernel.
  */
+#include <utility>
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
 
-enum { EPI_MOD = 1, EPI_GELU = 2, EPI_RES = 4, EPI_F16 = 8 };
+enum { EPI_MOD = 1, EPI_GELU = 2, EPI_RES = 4, EPI_F16 = 8, EPI_W = 16, EPI_B = 32, EPI_MADD = 64 };
 
 struct NormArgs {
     void *y;
@@ -38,11 +48,11 @@ struct NormArgs {
 };
 
 template <int NORM>
-__device__ __forceinline__ float norm_elem(float xv, float inv, double mu, double rstd, bool hw, float w,
+__device__ __forceinline__ float norm_elem(float xv, float inv, float mu, float rstd, bool hw, float w,
                                            bool hb, float b) {
     float n;
     if (NORM == ARIA_NORM_LAYER) {
-        n = (float)(((double)xv - mu) * rstd);
+        n = (xv - mu) * rstd;
         if (hw) n = n * w;
         if (hb) n = n + b;
     } else if (NORM == ARIA_NORM_GEMMA) {
@@ -50,6 +60,23 @@ __device__ __forceinline__ float norm_elem(float xv, float inv, double mu, doubl
     } else {
         n = xv * inv;
         if (hw) n = n * w;
+    }
+    return n;
+}
+
+template <int NORM, int EPI>
+__device__ __forceinline__ float norm_elem_c(float xv, float inv, float mu, float rstd, float w, float b) {
+    float n;
+    if (NORM == ARIA_NORM_LAYER) {
+        n = (xv - mu) * rstd;
+        if (EPI & EPI_W) n = n * w;
+        if (EPI & EPI_B) n = n + b;
+    } else if (NORM == ARIA_NORM_GEMMA) {
+        n = xv * inv;
+        if (EPI & EPI_W) n = n * (1.0f + w);
+    } else {
+        n = xv * inv;
+        if (EPI & EPI_W) n = n * w;
     }
     return n;
 }
@@ -84,7 +111,7 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
      * latency overlaps the row's instead of following it */
     const float4 *w4 = reinterpret_cast<const float4 *>(a.w);
     const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
-    const bool hw = a.w != nullptr, hb = a.b != nullptr;
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 wv[VPL], bv[VPL], scv[VPL], shv[VPL];
     {
         const float4 *sc4 = nullptr, *sh4 = nullptr, *sca4 = nullptr, *sha4 = nullptr;
@@ -92,7 +119,7 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
             const int bt = row / a.rows_per_batch;
             sc4 = reinterpret_cast<const float4 *>(a.scale + (size_t)bt * a.mod_bs);
             sh4 = reinterpret_cast<const float4 *>(a.shift + (size_t)bt * a.mod_bs);
-            if (a.scale_add) {
+            if (EPI & EPI_MADD) {
                 sca4 = reinterpret_cast<const float4 *>(a.scale_add + (size_t)bt * a.add_bs);
                 sha4 = reinterpret_cast<const float4 *>(a.shift_add + (size_t)bt * a.add_bs);
             }
@@ -100,13 +127,12 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
 #pragma unroll
         for (int j = 0; j < VPL; j++) {
             const int c4 = j * LPR + l;
-            wv[j] = hw ? w4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-            bv[j] = hb ? b4[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-            scv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-            shv[j] = scv[j];
+            wv[j] = (EPI & EPI_W) ? w4[c4] : z4;
+            bv[j] = (EPI & EPI_B) ? b4[c4] : z4;
+            scv[j] = z4; shv[j] = z4;
             if (EPI & EPI_MOD) {
                 scv[j] = sc4[c4]; shv[j] = sh4[c4];
-                if (sca4) {
+                if (EPI & EPI_MADD) {
                     const float4 sa = sca4[c4], ha = sha4[c4];
                     scv[j] = make_float4(scv[j].x + sa.x, scv[j].y + sa.y, scv[j].z + sa.z, scv[j].w + sa.w);
                     shv[j] = make_float4(shv[j].x + ha.x, shv[j].y + ha.y, shv[j].z + ha.z, shv[j].w + ha.w);
@@ -115,24 +141,22 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
         }
     }
 
-    float inv = 0.0f;
-    double mu = 0.0, rstd = 0.0;
+    float inv = 0.0f, mu = 0.0f, rstd = 0.0f;
     if (NORM == ARIA_NORM_LAYER) {
-        double s = 0.0;
+        float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < VPL; j++)
-            s += ((double)v[j].x + (double)v[j].y) + ((double)v[j].z + (double)v[j].w);
+        for (int j = 0; j < VPL; j++) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
         s = grp_sum<LPR>(s);
-        mu = s / dim;
-        double q = 0.0;
+        mu = s / (float)dim;
+        float q = 0.0f;
 #pragma unroll
         for (int j = 0; j < VPL; j++) {
-            double d0 = (double)v[j].x - mu, d1 = (double)v[j].y - mu;
-            double d2 = (double)v[j].z - mu, d3 = (double)v[j].w - mu;
-            q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+            const float d0 = v[j].x - mu, d1 = v[j].y - mu, d2 = v[j].z - mu, d3 = v[j].w - mu;
+            q = __builtin_fmaf(d0, d0, q); q = __builtin_fmaf(d1, d1, q);
+            q = __builtin_fmaf(d2, d2, q); q = __builtin_fmaf(d3, d3, q);
         }
         q = grp_sum<LPR>(q);
-        rstd = 1.0 / sqrt(q / dim + (double)a.eps);
+        rstd = __builtin_amdgcn_rsqf(q / (float)dim + a.eps);
     } else {
         double s = 0.0;
 #pragma unroll
@@ -148,10 +172,10 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
     for (int j = 0; j < VPL; j++) {
         const int c4 = j * LPR + l;
         float4 o;
-        o.x = epi_elem<EPI>(norm_elem<NORM>(v[j].x, inv, mu, rstd, hw, wv[j].x, hb, bv[j].x), v[j].x, scv[j].x, shv[j].x);
-        o.y = epi_elem<EPI>(norm_elem<NORM>(v[j].y, inv, mu, rstd, hw, wv[j].y, hb, bv[j].y), v[j].y, scv[j].y, shv[j].y);
-        o.z = epi_elem<EPI>(norm_elem<NORM>(v[j].z, inv, mu, rstd, hw, wv[j].z, hb, bv[j].z), v[j].z, scv[j].z, shv[j].z);
-        o.w = epi_elem<EPI>(norm_elem<NORM>(v[j].w, inv, mu, rstd, hw, wv[j].w, hb, bv[j].w), v[j].w, scv[j].w, shv[j].w);
+        o.x = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].x, inv, mu, rstd, wv[j].x, bv[j].x), v[j].x, scv[j].x, shv[j].x);
+        o.y = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].y, inv, mu, rstd, wv[j].y, bv[j].y), v[j].y, scv[j].y, shv[j].y);
+        o.z = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].z, inv, mu, rstd, wv[j].z, bv[j].z), v[j].z, scv[j].z, shv[j].z);
+        o.w = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].w, inv, mu, rstd, wv[j].w, bv[j].w), v[j].w, scv[j].w, shv[j].w);
         if (EPI & EPI_F16) {
             uint2 p;
             p.x = (uint32_t)f2h_bits(o.x) | ((uint32_t)f2h_bits(o.y) << 16);
@@ -171,17 +195,16 @@ __global__ __launch_bounds__(256) void k_rownorm_g(NormArgs a) {
     if (row >= a.rows) return;
     const int dim = a.dim;
     const float *xr = a.x + (size_t)row * dim;
-    float inv = 0.0f;
-    double mu = 0.0, rstd = 0.0;
+    float inv = 0.0f, mu = 0.0f, rstd = 0.0f;
     if (NORM == ARIA_NORM_LAYER) {
-        double s = 0.0;
-        for (int c = lane; c < dim; c += 64) s += (double)xr[c];
+        float s = 0.0f;
+        for (int c = lane; c < dim; c += 64) s += xr[c];
         s = grp_sum<64>(s);
-        mu = s / dim;
-        double q = 0.0;
-        for (int c = lane; c < dim; c += 64) { double d = (double)xr[c] - mu; q += d * d; }
+        mu = s / (float)dim;
+        float q = 0.0f;
+        for (int c = lane; c < dim; c += 64) { const float d = xr[c] - mu; q = __builtin_fmaf(d, d, q); }
         q = grp_sum<64>(q);
-        rstd = 1.0 / sqrt(q / dim + (double)a.eps);
+        rstd = __builtin_amdgcn_rsqf(q / (float)dim + a.eps);
     } else {
         double s = 0.0;
         for (int c = lane; c < dim; c += 64) s += (double)xr[c] * (double)xr[c];
@@ -216,21 +239,29 @@ __global__ __launch_bounds__(256) void k_rownorm_g(NormArgs a) {
 
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
-template <int NORM, int VPL, int LPR>
-static void launch_v(const NormArgs &a, int epi, hipStream_t s) {
+/* the operand sets instantiated for the register path, per norm */
+using EpiRms = std::integer_sequence<int, 0, EPI_W, EPI_F16, EPI_F16 | EPI_W, EPI_MOD | EPI_W, EPI_MOD | EPI_F16 | EPI_W,
+                                      EPI_MOD | EPI_MADD | EPI_W, EPI_MOD | EPI_MADD | EPI_F16 | EPI_W>;
+using EpiGemma = std::integer_sequence<int, 0, EPI_W>;
+using EpiLayer = std::integer_sequence<int, 0, EPI_W, EPI_B, EPI_W | EPI_B, EPI_MOD | EPI_GELU | EPI_RES,
+                                        EPI_MOD | EPI_GELU | EPI_RES | EPI_W | EPI_B>;
+template <int NORM> struct EpiSet;
+template <> struct EpiSet<ARIA_NORM_RMS> { using type = EpiRms; };
+template <> struct EpiSet<ARIA_NORM_GEMMA> { using type = EpiGemma; };
+template <> struct EpiSet<ARIA_NORM_LAYER> { using type = EpiLayer; };
+
+template <int NORM, int VPL, int LPR, int E>
+static bool launch_v1(const NormArgs &a, int epi, hipStream_t s) {
+    if (epi != E) return false;
     constexpr int RPW = ARIA_WAVE / LPR;
-    dim3 grid((a.rows + 4 * RPW - 1) / (4 * RPW)), blk(256);
-    switch (epi) {
-        case 0: hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, 0>), grid, blk, 0, s, a); break;
-        case EPI_F16: hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, EPI_F16>), grid, blk, 0, s, a); break;
-        case EPI_MOD: hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, EPI_MOD>), grid, blk, 0, s, a); break;
-        case EPI_MOD | EPI_F16:
-            hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, EPI_MOD | EPI_F16>), grid, blk, 0, s, a); break;
-        case EPI_MOD | EPI_GELU | EPI_RES:
-            hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, EPI_MOD | EPI_GELU | EPI_RES>), grid, blk, 0, s, a);
-            break;
-        default: hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), blk, 0, s, a); break;
-    }
+    hipLaunchKernelGGL((k_rownorm_v<NORM, VPL, LPR, E>), dim3((a.rows + 4 * RPW - 1) / (4 * RPW)), dim3(256), 0, s, a);
+    return true;
+}
+
+/* launches k_rownorm_v<NORM, VPL, LPR, epi> if epi is in the set; false otherwise */
+template <int NORM, int VPL, int LPR, int... E>
+static bool launch_v(const NormArgs &a, int epi, hipStream_t s, std::integer_sequence<int, E...>) {
+    return (launch_v1<NORM, VPL, LPR, E>(a, epi, s) || ...);
 }
 
 template <int NORM>
@@ -240,24 +271,24 @@ static hipError_t launch_norm(const NormArgs &a, hipStream_t s) {
                      (!a.w || al16(a.w)) && (!a.b || al16(a.b)) && (!a.scale || al16(a.scale)) &&
                      (!a.shift || al16(a.shift)) && (!a.scale_add || al16(a.scale_add)) &&
                      (!a.shift_add || al16(a.shift_add)) && a.mod_bs % 4 == 0 && a.add_bs % 4 == 0;
-    int epi = (a.scale ? EPI_MOD : 0) | (a.gelu ? EPI_GELU : 0) | (a.resid ? EPI_RES : 0) | (a.f16 ? EPI_F16 : 0);
-    /* only these epilogues are instantiated for the register path; others take the generic kernel */
-    const bool known = epi == 0 || epi == EPI_F16 || epi == EPI_MOD || epi == (EPI_MOD | EPI_F16) ||
-                       epi == (EPI_MOD | EPI_GELU | EPI_RES);
-    if (!vec || !known) {
-        hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), dim3(256), 0, s, a);
-        return hipGetLastError();
+    const int epi = (a.scale ? EPI_MOD : 0) | (a.gelu ? EPI_GELU : 0) | (a.resid ? EPI_RES : 0) |
+                    (a.f16 ? EPI_F16 : 0) | (a.w ? EPI_W : 0) | (a.b ? EPI_B : 0) |
+                    (a.scale && a.scale_add ? EPI_MADD : 0);
+    using Set = typename EpiSet<NORM>::type;
+    bool hit = false;
+    if (vec) {
+        switch (dim) {
+            case 64: hit = launch_v<NORM, 1, 16>(a, epi, s, Set{}); break;
+            case 128: hit = launch_v<NORM, 1, 32>(a, epi, s, Set{}); break;
+            case 256: hit = launch_v<NORM, 1, 64>(a, epi, s, Set{}); break;
+            case 512: hit = launch_v<NORM, 2, 64>(a, epi, s, Set{}); break;
+            case 768: hit = launch_v<NORM, 3, 64>(a, epi, s, Set{}); break;
+            case 1024: hit = launch_v<NORM, 4, 64>(a, epi, s, Set{}); break;
+            case 2048: hit = launch_v<NORM, 8, 64>(a, epi, s, Set{}); break;
+            default: break;
+        }
     }
-    switch (dim) {
-        case 64: launch_v<NORM, 1, 16>(a, epi, s); break;
-        case 128: launch_v<NORM, 1, 32>(a, epi, s); break;
-        case 256: launch_v<NORM, 1, 64>(a, epi, s); break;
-        case 512: launch_v<NORM, 2, 64>(a, epi, s); break;
-        case 768: launch_v<NORM, 3, 64>(a, epi, s); break;
-        case 1024: launch_v<NORM, 4, 64>(a, epi, s); break;
-        case 2048: launch_v<NORM, 8, 64>(a, epi, s); break;
-        default: hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), dim3(256), 0, s, a); break;
-    }
+    if (!hit) hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

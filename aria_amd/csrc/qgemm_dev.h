@@ -64,8 +64,12 @@ __device__ __forceinline__ int xcd_tile(int g, int T) {
  * 16 B per lane, coalesced. acc register r of lane l holds n = 8*(r/4) + 4*(l/32) + r%4,
  * m = l%32 of its block. E is this wave's staging area (32 rows of 32*FN*4 + 16 bytes);
  * mw / nw are the first activation row and the first weight row of the wave's tile.
- * v = acc * scale (Q8) + bias, GELU'd when a.gelu, then the fused mode MODE (compile
- * time; EPI_ANY dispatches on a.epi.mode at run time). Every global load of a 32-row
+ * v = acc * scale (Q8) + bias, GELU'd when GELU, then the fused mode MODE (both compile
+ * time; EPI_ANY dispatches on a.epi.mode and a.gelu once per call). A run-time GELU flag
+ * inside the element loop is if-converted by the compiler: every output then pays the
+ * GELU and a select whether or not it is wanted. Without a bias the lane adds -0.0,
+ * which leaves every value (signed zeros and NaN included) unchanged, so the bias needs
+ * neither a branch nor a select. Every global load of a 32-row
  * group (residual, gate, local cond, RoPE tables) is issued before its first store:
  * loads and stores retire in order, so a load issued after a store would make the next
  * wait cover that store's whole write latency.
@@ -73,7 +77,7 @@ __device__ __forceinline__ int xcd_tile(int g, int T) {
  * head-aligned); the arithmetic is k_qkv_prep's (k_attn.hip): RMS statistic in fp32
  * over the head, (x * inv) * w, then rotate-half RoPE over the first rot dims. */
 #define EPI_ANY (-1)
-template <int FM, int FN, int WT, int MODE>
+template <int FM, int FN, int WT, int MODE, bool GELU = false>
 __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN], float *E, int lane, int mw, int nw) {
     constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
     constexpr int CW = 32 * FN;                 /* columns per wave */
@@ -81,12 +85,27 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
     constexpr int RPI = 64 / LPR;               /* rows per store instruction */
     constexpr int NIT = 32 / RPI;               /* store instructions per 32-row group */
     if constexpr (MODE == EPI_ANY) {
+        const bool g = a.gelu != 0;
         switch (a.epi.mode) {
-            case ARIA_EPI_GATE_RES: epilogue<FM, FN, WT, ARIA_EPI_GATE_RES>(a, acc, E, lane, mw, nw); return;
-            case ARIA_EPI_ADD: epilogue<FM, FN, WT, ARIA_EPI_ADD>(a, acc, E, lane, mw, nw); return;
-            case ARIA_EPI_HEADS: if constexpr (LPR % 16 == 0) epilogue<FM, FN, WT, ARIA_EPI_HEADS>(a, acc, E, lane, mw, nw); return;
-            case ARIA_EPI_GLU: epilogue<FM, FN, WT, ARIA_EPI_GLU>(a, acc, E, lane, mw, nw); return;
-            default: epilogue<FM, FN, WT, ARIA_EPI_STORE>(a, acc, E, lane, mw, nw); return;
+            case ARIA_EPI_GATE_RES:
+                if (g) epilogue<FM, FN, WT, ARIA_EPI_GATE_RES, true>(a, acc, E, lane, mw, nw);
+                else epilogue<FM, FN, WT, ARIA_EPI_GATE_RES>(a, acc, E, lane, mw, nw);
+                return;
+            case ARIA_EPI_ADD:
+                if (g) epilogue<FM, FN, WT, ARIA_EPI_ADD, true>(a, acc, E, lane, mw, nw);
+                else epilogue<FM, FN, WT, ARIA_EPI_ADD>(a, acc, E, lane, mw, nw);
+                return;
+            case ARIA_EPI_HEADS:
+                if constexpr (LPR % 16 == 0) {
+                    if (g) epilogue<FM, FN, WT, ARIA_EPI_HEADS, true>(a, acc, E, lane, mw, nw);
+                    else epilogue<FM, FN, WT, ARIA_EPI_HEADS>(a, acc, E, lane, mw, nw);
+                }
+                return;
+            case ARIA_EPI_GLU: epilogue<FM, FN, WT, ARIA_EPI_GLU>(a, acc, E, lane, mw, nw); return;   /* no GELU */
+            default:
+                if (g) epilogue<FM, FN, WT, ARIA_EPI_STORE, true>(a, acc, E, lane, mw, nw);
+                else epilogue<FM, FN, WT, ARIA_EPI_STORE>(a, acc, E, lane, mw, nw);
+                return;
         }
     } else {
     static_assert(MODE != ARIA_EPI_HEADS || LPR % 16 == 0, "a head's 64 columns must sit in one wave");
@@ -94,7 +113,7 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
     const int ecol = (lane % LPR) * 4, erow = lane / LPR;
     const int nb = nw + ecol;                   /* this lane's 4 output columns */
     const bool col_ok = nb < a.N;
-    float4 sc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), bb = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 sc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), bb = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
     if (col_ok) {
         if (WT == ARIA_WQ8) sc = *reinterpret_cast<const float4 *>(a.scale + nb);
         if (a.bias) bb = *reinterpret_cast<const float4 *>(a.bias + nb);
@@ -170,8 +189,8 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 if (WT == ARIA_WQ8) v[it][q] = v[it][q] * scv[q];
-                if (a.bias) v[it][q] = v[it][q] + bv[q];
-                if (a.gelu) v[it][q] = gelu_tanh_f(v[it][q]);
+                v[it][q] = v[it][q] + bv[q];
+                if constexpr (GELU) v[it][q] = gelu_tanh_f(v[it][q]);
             }
         }
         __builtin_amdgcn_wave_barrier();   /* staging reads done before the next group's writes */

@@ -63,6 +63,9 @@ def parse():
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: each C2 op a few times with no events in between, plus one "
                          "256 MiB device-to-device copy whose FETCH/WRITE counters calibrate the others")
+    ap.add_argument("--pmc-gemm", action="store_true",
+                    help="for rocprofv3 --pmc: the config-3 GEMMs (5 launches each) and two forwards of each "
+                         "config-4 block variant, untimed")
     return ap.parse_args()
 
 
@@ -153,6 +156,16 @@ def main():
     print(f"[bench] device: {aria_amd.device_info()}", file=sys.stderr, flush=True)
 
     rng = np.random.default_rng(SEED)
+    if args.pmc_gemm:
+        def run_only(fn, reps):
+            for i in range(reps):
+                chk(fn(i))
+            chk(L.aria_hip_stream_sync(stream))
+            return 1.0
+        gemm_leg(L, chk, DeviceArray, run_only, stream, rng, 2)
+        block_leg(DeviceArray, run_only, stream, rng, 2)
+        print(json.dumps({"pmc_gemm": True}), flush=True)
+        return
     x = rng.standard_normal((B, S, D), dtype=np.float32)
     sc = (0.1 * rng.standard_normal((B, D))).astype(np.float32)
     sh = (0.1 * rng.standard_normal((B, D))).astype(np.float32)
