@@ -62,26 +62,41 @@ __device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t mask, uint32_t m
 
 /* the 8 fp16 weights of block j for MFMA step ks. Q4: a dword holds 8 nibbles, byte b =
  * (k = 2b low, k = 2b + 1 high). Each nibble is placed under the fp16 exponent of 1024
- * (0x6400 | n = 1024 + n; the high nibble of a byte lands as 1024 + 16 n), 1024 is
- * subtracted exactly, and a mixed-precision FMA (fp16 operand, fp32 arithmetic, fp16
- * result) forms min + n * step (step / 16 for the high nibbles, an exact power-of-two
- * scaling): the value the reference dequantizes, rounded to fp16. */
+ * (0x6400 | n = 1024 + n; the high nibble of a byte lands as 1024 + 16 n) and a
+ * mixed-precision FMA (fp16 operand, fp32 arithmetic, fp16 result) forms
+ * (1024 + n) * step + (min - 1024 step) = min + n * step (step / 16 and min - 64 step for
+ * the high nibbles): the value the reference dequantizes, rounded to fp16. The two offsets
+ * are formed once per block and K-tile (off[j]), so the 1024 never has to be subtracted
+ * from the nibbles (4 packed subtractions per step); the fp32 offset carries ~2e-7 absolute
+ * error per weight before the fp16 rounding. */
+struct Q4Off { float a, b, st, s16; };
 template <int WT>
-__device__ __forceinline__ half8_t wr_frag(const WRegs<WT> &s, int j, int ks, uint32_t magic) {
+__device__ __forceinline__ Q4Off q4_off(const WRegs<WT> &s, int j) {
+    Q4Off o;
+    if constexpr (WT == ARIA_WQ4) {
+        const float mn = __builtin_bit_cast(float, s.w[j][4]);
+        o.st = __builtin_bit_cast(float, s.w[j][5]);
+        o.s16 = o.st * 0.0625f;
+        o.a = __builtin_fmaf(-1024.0f, o.st, mn);
+        o.b = __builtin_fmaf(-64.0f, o.st, mn);
+    } else {
+        o.a = o.b = o.st = o.s16 = 0.0f;
+    }
+    return o;
+}
+template <int WT>
+__device__ __forceinline__ half8_t wr_frag(const WRegs<WT> &s, int j, int ks, uint32_t magic, const Q4Off &f) {
     uint32_t o[4];
     if (WT == ARIA_WQ4) {
         const uint32_t w = s.w[j][ks], u = w >> 8;
-        const float mn = __builtin_bit_cast(float, s.w[j][4]), st = __builtin_bit_cast(float, s.w[j][5]);
-        const float s16 = st * 0.0625f;
-        const half2_t bias = {(_Float16)1024.0f, (_Float16)1024.0f};
-        const half2_t t0 = __builtin_bit_cast(half2_t, and_or(w, 0x000F000Fu, magic)) - bias;   /* k0, k4 */
-        const half2_t t1 = __builtin_bit_cast(half2_t, and_or(w, 0x00F000F0u, magic)) - bias;   /* 16 k1, 16 k5 */
-        const half2_t t2 = __builtin_bit_cast(half2_t, and_or(u, 0x000F000Fu, magic)) - bias;   /* k2, k6 */
-        const half2_t t3 = __builtin_bit_cast(half2_t, and_or(u, 0x00F000F0u, magic)) - bias;   /* 16 k3, 16 k7 */
-        const half2_t h0 = {(_Float16)__builtin_fmaf((float)t0[0], st, mn), (_Float16)__builtin_fmaf((float)t1[0], s16, mn)};
-        const half2_t h1 = {(_Float16)__builtin_fmaf((float)t2[0], st, mn), (_Float16)__builtin_fmaf((float)t3[0], s16, mn)};
-        const half2_t h2 = {(_Float16)__builtin_fmaf((float)t0[1], st, mn), (_Float16)__builtin_fmaf((float)t1[1], s16, mn)};
-        const half2_t h3 = {(_Float16)__builtin_fmaf((float)t2[1], st, mn), (_Float16)__builtin_fmaf((float)t3[1], s16, mn)};
+        const half2_t t0 = __builtin_bit_cast(half2_t, and_or(w, 0x000F000Fu, magic));   /* 1024 + k0, k4 */
+        const half2_t t1 = __builtin_bit_cast(half2_t, and_or(w, 0x00F000F0u, magic));   /* 1024 + 16 k1, 16 k5 */
+        const half2_t t2 = __builtin_bit_cast(half2_t, and_or(u, 0x000F000Fu, magic));   /* 1024 + k2, k6 */
+        const half2_t t3 = __builtin_bit_cast(half2_t, and_or(u, 0x00F000F0u, magic));   /* 1024 + 16 k3, 16 k7 */
+        const half2_t h0 = {(_Float16)__builtin_fmaf((float)t0[0], f.st, f.a), (_Float16)__builtin_fmaf((float)t1[0], f.s16, f.b)};
+        const half2_t h1 = {(_Float16)__builtin_fmaf((float)t2[0], f.st, f.a), (_Float16)__builtin_fmaf((float)t3[0], f.s16, f.b)};
+        const half2_t h2 = {(_Float16)__builtin_fmaf((float)t0[1], f.st, f.a), (_Float16)__builtin_fmaf((float)t1[1], f.s16, f.b)};
+        const half2_t h3 = {(_Float16)__builtin_fmaf((float)t2[1], f.st, f.a), (_Float16)__builtin_fmaf((float)t3[1], f.s16, f.b)};
         o[0] = __builtin_bit_cast(uint32_t, h0); o[1] = __builtin_bit_cast(uint32_t, h1);
         o[2] = __builtin_bit_cast(uint32_t, h2); o[3] = __builtin_bit_cast(uint32_t, h3);
     } else {
@@ -162,9 +177,10 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_wr(QArgs a, int NTN, int T)
 #pragma unroll
             for (int e = 0; e < WRegs<WT>::NW; e++) asm volatile("" : "+v"(ws.w[j][e]));
         const uint16_t *X = lds + buf * (BM * WBK);
+        const Q4Off f0 = q4_off<WT>(ws, 0), f1 = q4_off<WT>(ws, 1);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const half8_t w0 = wr_frag<WT>(ws, 0, ks, magic), w1 = wr_frag<WT>(ws, 1, ks, magic);
+            const half8_t w0 = wr_frag<WT>(ws, 0, ks, magic, f0), w1 = wr_frag<WT>(ws, 1, ks, magic, f1);
 #pragma unroll
             for (int i = 0; i < FM; i++) {
                 const half8_t xf = *reinterpret_cast<const half8_t *>(&X[xoff(i * 32 + lrow, 4 * lh + ks)]);
