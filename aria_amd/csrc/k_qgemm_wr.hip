@@ -106,7 +106,16 @@ __device__ __forceinline__ half8_t wr_frag(const WRegs<WT> &s, int j, int ks, ui
     return __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-template <int WT, int FM, int MINB, int MODE, bool GELU>
+/* f(IC<0>{}), ..., f(IC<N-1>{}) */
+template <int N, int I = 0, class Fn>
+__device__ __forceinline__ void static_for(Fn &&f) {
+    if constexpr (I < N) {
+        f(IC<I>{});
+        static_for<N, I + 1>(f);
+    }
+}
+
+template <int WT, int FM, int MINB, int MODE, bool GELU, int DP = (WT == ARIA_WQ8 && FM >= 3 ? 3 : 2)>
 __global__ __launch_bounds__(256, MINB) void k_qgemm_wr(QArgs a, int NTN, int T) {
     constexpr int FN = 2, BM = 32 * FM, BN = 256;
     constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
@@ -126,18 +135,22 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_wr(QArgs a, int NTN, int T)
 
     /* activation staging: thread tid moves chunk c = tid + 256 i (row c / 8, chunk c % 8);
      * rows past M re-read the last row (their results are never stored). Tile t is staged
-     * in register set t & 1 (xa, xb), loaded two K-tiles before it is stored to LDS.
-     * Weights of tile t sit in stage t % 3 (s0, s1, s2), also loaded two K-tiles ahead.
-     * Sets and stages are picked by compile-time constants (IC<>) so they stay in VGPRs. */
+     * in register set t % DP (xa, xb, xc), loaded DP K-tiles before it is multiplied and
+     * stored to LDS one K-tile before. Weights of tile t sit in stage t % (DP + 1)
+     * (s0 .. s3), also loaded DP K-tiles ahead. Sets and stages are picked by compile-time
+     * constants (IC<>) so they stay in VGPRs. */
+    static_assert(DP == 2 || DP == 3, "prefetch distance");
     typedef uint32_t xv_t __attribute__((ext_vector_type(4 * FM)));
-    xv_t xa, xb;
-    WRegs<WT> s0, s1, s2;
+    xv_t xa, xb, xc;
+    WRegs<WT> s0, s1, s2, s3;
     auto xsel = [&](auto XS) __attribute__((always_inline)) -> xv_t & {
-        if constexpr (decltype(XS)::value == 0) return xa; else return xb;
+        constexpr int xs = decltype(XS)::value;
+        if constexpr (xs == 0) return xa; else if constexpr (xs == 1) return xb; else return xc;
     };
     auto wsel = [&](auto ST) __attribute__((always_inline)) -> WRegs<WT> & {
         constexpr int st = decltype(ST)::value;
-        if constexpr (st == 0) return s0; else if constexpr (st == 1) return s1; else return s2;
+        if constexpr (st == 0) return s0; else if constexpr (st == 1) return s1;
+        else if constexpr (st == 2) return s2; else return s3;
     };
     auto xload = [&](auto XS, int kt) __attribute__((always_inline)) {
         xv_t &xr = xsel(XS);
@@ -196,45 +209,43 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_wr(QArgs a, int NTN, int T)
         xload(IC<1>{}, 1);
         wr_load<WT>(a, s1, nrow, 1, lh);
     }
+    if constexpr (DP == 3) {
+        if (KT > 2) {
+            xload(IC<2>{}, 2);
+            wr_load<WT>(a, s2, nrow, 2, lh);
+        }
+    }
     xstore(IC<0>{}, 0);
     /* drain the prologue's loads: the loop header then inherits only the steady-state
      * wait counts (otherwise the merged state makes the first step of every iteration
      * wait for loads issued one step earlier) */
     __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
     __syncthreads();
-    /* step kt (kt % 6 == P): tile kt+2 loaded (weights into stage (P+2) % 3, activations
-     * into set P & 1), tile kt multiplied out of LDS buffer P & 1 with stage P % 3, tile
-     * kt+1 stored from set (P+1) & 1 into the other buffer. GUARD: the tail form. */
+    /* step kt (kt % U == P): tile kt+DP loaded (weights into stage (P+DP) % (DP+1),
+     * activations into set P % DP), tile kt multiplied out of LDS buffer P & 1 with stage
+     * P % (DP+1), tile kt+1 stored from set (P+1) % DP into the other buffer. GUARD: the
+     * tail form. U = lcm(DP + 1, DP, 2) steps are unrolled so every index is a constant. */
+    constexpr int U = DP == 2 ? 6 : 12;
     auto step = [&](auto PP, auto GUARD, int kt) __attribute__((always_inline)) {
         constexpr int P = decltype(PP)::value;
         constexpr bool guard = decltype(GUARD)::value;
-        if (!guard || kt + 2 < KT) {
-            wr_load<WT>(a, wsel(IC<(P + 2) % 3>{}), nrow, kt + 2, lh);
-            xload(IC<P & 1>{}, kt + 2);
+        if (!guard || kt + DP < KT) {
+            wr_load<WT>(a, wsel(IC<(P + DP) % (DP + 1)>{}), nrow, kt + DP, lh);
+            xload(IC<P % DP>{}, kt + DP);
         }
-        compute(IC<P % 3>{}, P & 1);
-        if (!guard || kt + 1 < KT) xstore(IC<(P + 1) & 1>{}, (P + 1) & 1);
+        compute(IC<P % (DP + 1)>{}, P & 1);
+        if (!guard || kt + 1 < KT) xstore(IC<(P + 1) % DP>{}, (P + 1) & 1);
         __syncthreads();
     };
     using F = std::false_type;
     using G = std::true_type;
     int kt = 0;
-    for (; kt + 8 <= KT; kt += 6) {
-        step(IC<0>{}, F{}, kt);
-        step(IC<1>{}, F{}, kt + 1);
-        step(IC<2>{}, F{}, kt + 2);
-        step(IC<3>{}, F{}, kt + 3);
-        step(IC<4>{}, F{}, kt + 4);
-        step(IC<5>{}, F{}, kt + 5);
-    }
-    for (; kt < KT; kt += 6) {
-        step(IC<0>{}, G{}, kt);
-        if (kt + 1 < KT) step(IC<1>{}, G{}, kt + 1);
-        if (kt + 2 < KT) step(IC<2>{}, G{}, kt + 2);
-        if (kt + 3 < KT) step(IC<3>{}, G{}, kt + 3);
-        if (kt + 4 < KT) step(IC<4>{}, G{}, kt + 4);
-        if (kt + 5 < KT) step(IC<5>{}, G{}, kt + 5);
-    }
+    for (; kt + U + DP <= KT; kt += U)
+        static_for<U>([&](auto PP) __attribute__((always_inline)) { step(PP, F{}, kt + decltype(PP)::value); });
+    for (; kt < KT; kt += U)
+        static_for<U>([&](auto PP) __attribute__((always_inline)) {
+            if (kt + decltype(PP)::value < KT) step(PP, G{}, kt + decltype(PP)::value);
+        });
 
     float *E = reinterpret_cast<float *>(lds) + wave * (32 * EPI_STRIDE / 4);
     epilogue<FM, FN, WT, MODE, GELU>(a, acc, E, lane, m0, n0 + wave * 64);
