@@ -334,15 +334,18 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
     }
     __syncthreads();
     /* two tiles per trip so each LDS buffer is a fixed address; buffer b^1 was last read
-     * one tile earlier, before that tile's closing barrier */
+     * one tile earlier, before that tile's closing barrier. A wave whose 32 queries all lie
+     * past Nq (the tail of the last query block: 1296 = 10 x 128 + 16) only stages tiles and
+     * meets the barriers; its products would never be stored. */
+    const bool live = q0 < a.Nq;
     for (int t = 0; t < niter; t += 2) {
         if (t + 1 < nt) gload(kbase + (t + 1) * KT);
-        if (t < nt) tile(kbase + t * KT, K0, V0);
+        if (live && t < nt) tile(kbase + t * KT, K0, V0);
         if (t + 1 < nt) sstore(1);
         __syncthreads();
         if (t + 1 < niter) {
             if (t + 2 < nt) gload(kbase + (t + 2) * KT);
-            if (t + 1 < nt) tile(kbase + (t + 1) * KT, K1, V1);
+            if (live && t + 1 < nt) tile(kbase + (t + 1) * KT, K1, V1);
             if (t + 2 < nt) sstore(0);
             __syncthreads();
         }
@@ -363,7 +366,8 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
         __syncthreads();
         if (half == 1) return;
         const float m1 = X[33 * 64], l1 = X[32 * 64];
-        const float m = fmaxf(m_use, m1);   /* half 0 always has keys: m is finite */
+        const float m = fmaxf(m_use, m1);   /* finite for a live wave (half 0 always has keys); a
+                                             * wave past Nq returns below without storing */
         const float a0 = __builtin_amdgcn_exp2f(m_use - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
