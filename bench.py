@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import statistics
 import os
 import sys
 import time
@@ -161,7 +162,7 @@ def main():
             for i in range(reps):
                 chk(fn(i))
             chk(L.aria_hip_stream_sync(stream))
-            return 1.0
+            return 1.0, 1.0
         gemm_leg(L, chk, DeviceArray, run_only, stream, rng, 2)
         block_leg(DeviceArray, run_only, stream, rng, 2)
         print(json.dumps({"pmc_gemm": True}), flush=True)
@@ -225,15 +226,21 @@ def main():
             chk(run_op(op, sets[i % len(sets)]), op)
     chk(L.aria_hip_stream_sync(stream))
 
-    def time_loop(fn, reps):
-        """average ms of fn(i) over reps back-to-back launches, HIP events on the launch stream"""
-        tm = Timer(stream)
-        chk(fn(0))                          # first launch loads the code object
-        chk(L.aria_hip_stream_sync(stream))
-        tm.start()
-        for i in range(reps):
+    def time_loop(fn, reps, trials=5):
+        """(median, min) over `trials` of the average ms of fn(i) over `reps` back-to-back
+        launches, HIP events on the launch stream, after 3 untimed launches (the first loads
+        the code object)"""
+        for i in range(3):
             chk(fn(i))
-        return tm.stop() / reps
+        chk(L.aria_hip_stream_sync(stream))
+        res = []
+        for _ in range(trials):
+            tm = Timer(stream)
+            tm.start()
+            for i in range(reps):
+                chk(fn(i))
+            res.append(tm.stop() / reps)
+        return statistics.median(res), min(res)
 
     # timed region (value): K whole steps, events only around them
     tmr = Timer(stream)
@@ -253,12 +260,12 @@ def main():
     reps = max(args.steps, 20)
     ops_report = {}
     for op in OPS:
-        avg = time_loop(lambda i, op=op: run_op(op, sets[i % len(sets)]), reps)
+        avg, _ = time_loop(lambda i, op=op: run_op(op, sets[i % len(sets)]), reps)
         ops_report[op] = {"us": round(avg * 1e3, 2), "GB/s": round(ab[op] / (avg * 1e-3) / 1e9, 1),
                           "bytes": ab[op], "frac_peak": round(ab[op] / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
 
     # extra: rot-32 RoPE (the DiT's), Q8/Q4 pack of W [4096, 1024]
-    ms = time_loop(lambda i: L.aria_hip_rope_apply2_dev(sets[i % len(sets)]["q"].p, sets[i % len(sets)]["k"].p,
+    ms, _ = time_loop(lambda i: L.aria_hip_rope_apply2_dev(sets[i % len(sets)]["q"].p, sets[i % len(sets)]["k"].p,
                                                         d_cos.p, d_sin.p, B * H, S, HD, 32, stream), reps)
     rope32_bytes = 2 * 2 * B * H * S * 32 * 4 + 2 * S * 16 * 4
     ops_report["rope_rot32"] = {"us": round(ms * 1e3, 2), "GB/s": round(rope32_bytes / (ms * 1e-3) / 1e9, 1),
@@ -271,7 +278,7 @@ def main():
     for name, fn, outb in (("q8_pack", L.aria_hip_q8_quant_dev, Wn * Wk + Wn * 4),
                            ("q4_pack", L.aria_hip_q4_quant_dev, Wn * Wk // 2 + Wn * 2 * (Wk // 32) * 4)):
         dq, ds = (d_q8, d_s8) if name == "q8_pack" else (d_q4, d_s4)
-        ms = time_loop(lambda i, fn=fn, dq=dq, ds=ds: fn(dq.p, ds.p, d_W[i % 8].p, Wn, Wk, stream), reps)
+        ms, _ = time_loop(lambda i, fn=fn, dq=dq, ds=ds: fn(dq.p, ds.p, d_W[i % 8].p, Wn, Wk, stream), reps)
         byt = Wn * Wk * 4 + outb
         ops_report[name] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / (ms * 1e-3) / 1e9, 1), "bytes": byt}
     del d_W
@@ -341,10 +348,10 @@ def gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps):
                                                                         None, M, K, N, stream))
             for i in range(3):
                 chk(fn(i))
-            ms = time_loop(fn, reps)
+            ms, ms_min = time_loop(fn, reps)
             tf = flop / (ms * 1e-3) / 1e12
             key = f"{'q8' if wt == 0 else 'q4'}_M{M}_K{K}_N{N}"
-            out[key] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+            out[key] = {"us": round(ms * 1e3, 2), "us_min": round(ms_min * 1e3, 2), "TFLOP/s": round(tf, 1),
                         "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 3), "flop": flop}
     return out
 
@@ -374,11 +381,12 @@ def block_leg(DeviceArray, time_loop, stream, rng, reps):
         def fwd(i):
             blk.forward(dx, Bb, Sb, dg, dk, dv, Sc, dcos, dsin, 32, ws=ws, stream=stream)
             return 0
-        ms = time_loop(fwd, reps)
+        ms, ms_min = time_loop(fwd, reps)
         ffrows = 2 * inner if ffn == FFN_GLU else inner
         flop = 2.0 * M * dim * (3 * dim + dim + dim + dim) + 2.0 * M * dim * (ffrows + inner) \
             + 2 * 2.0 * Bb * H * Sb * Sb * 64 + 2 * 2.0 * Bb * H * Sb * Sc * 64
-        out[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "flop": flop,
+        out[name] = {"us": round(ms * 1e3, 1), "us_min": round(ms_min * 1e3, 1),
+                     "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "flop": flop,
                      "weight_bytes": blk.weight_bytes}
         blk.free()
     return out
@@ -417,12 +425,17 @@ def dit_leg(DeviceArray, Timer, L, chk, stream, rng, steps=8, depth=24):
         L.aria_cuda_memcpy_h2d(dg, gall[0].ctypes.data, gall[0].nbytes)
         dit.run(stream)                      # first step captures the graph (graph mode)
         chk(L.aria_hip_stream_sync(stream))
-        tm = Timer(stream)
-        tm.start()
-        for i in range(steps):
-            chk(L.aria_hip_memcpy_d2d_async(dg, d_g[i].p, d_g[i].nbytes, stream))
-            dit.run(stream)
-        out[f"{mode}_ms_per_step"] = round(tm.stop() / steps, 3)
+        res = []
+        for _ in range(3):                   # median and min of three 8-step runs
+            L.aria_cuda_memcpy_h2d(dx, x0.ctypes.data, x0.nbytes)
+            tm = Timer(stream)
+            tm.start()
+            for i in range(steps):
+                chk(L.aria_hip_memcpy_d2d_async(dg, d_g[i].p, d_g[i].nbytes, stream))
+                dit.run(stream)
+            res.append(tm.stop() / steps)
+        out[f"{mode}_ms_per_step"] = round(statistics.median(res), 3)
+        out[f"{mode}_ms_per_step_min"] = round(min(res), 3)
         if mode == "graph":
             out["graph_active"] = dit.graph_active
             nz = np.random.default_rng(SEED + 5)
