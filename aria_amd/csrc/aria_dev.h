@@ -83,6 +83,14 @@ template <int G> __device__ __forceinline__ double grp_sum(double v) { return gr
 template <int G> __device__ __forceinline__ float grp_max(float v) { return grp_reduce<G>(v, OpMax()); }
 template <int G> __device__ __forceinline__ float grp_min(float v) { return grp_reduce<G>(v, OpMin()); }
 
+/* Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
+ * workgroup g runs on XCD g % 8. Tile t = (g % 8) * ceil(T/8) + g / 8 gives each XCD a
+ * contiguous run of tiles; launch a multiple of 8 workgroups and skip t >= T. */
+__device__ __forceinline__ int xcd_tile(int g, int T) {
+    const int per = (T + 7) >> 3;
+    return (g & 7) * per + (g >> 3);
+}
+
 /* ---- exp2-based transcendentals (v_exp_f32 / v_rcp_f32, ~1 ulp each) ----
  * exp(x) = 2^(x*log2 e); the rounding of x*log2 e gives a relative error of about
  * |x| * 4e-8, far inside the 1e-5 gates for the ranges these ops see. */

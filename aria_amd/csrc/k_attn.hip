@@ -135,6 +135,7 @@ struct AttnArgs {
     const uint16_t *q, *k, *v;   /* [B*H, N, 64] fp16 */
     void *o;                     /* [B, Nq, H*64] merged heads */
     int H, Nq, Nk;
+    int nqb, T;                  /* 128-query blocks per (batch, head); nqb * B*H */
     float scale_log2;            /* (1/sqrt(64)) * log2(e) */
     int o_f16;
 };
@@ -190,8 +191,12 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
     uint16_t *const Kb0 = smem + (half * 2) * (KT * 64), *const Kb1 = Kb0 + KT * 64;
     uint16_t *const Vb0 = smem + (KS * 2 + half * 2) * (KT * 64), *const Vb1 = Vb0 + KT * 64;
     const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
-    const int bh = blockIdx.y;
-    const int q0 = blockIdx.x * 128 + wave * 32;
+    /* the query blocks of one (batch, head) run on one XCD, so its K and V are fetched
+     * into that XCD's L2 once rather than into every XCD's */
+    const int tix = xcd_tile(blockIdx.x, a.T);
+    if (tix >= a.T) return;                 /* uniform per workgroup, before any barrier */
+    const int bh = tix / a.nqb;
+    const int q0 = (tix % a.nqb) * 128 + wave * 32;
     const uint16_t *Qh = a.q + (size_t)bh * a.Nq * 64;
     const uint16_t *Kh = a.k + (size_t)bh * a.Nk * 64;
     const uint16_t *Vh = a.v + (size_t)bh * a.Nk * 64;
@@ -407,7 +412,9 @@ extern "C" hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, co
     AttnArgs a;
     a.q = q; a.k = k; a.v = v; a.o = o; a.H = H; a.Nq = Nq; a.Nk = Nk; a.o_f16 = o_f16;
     a.scale_log2 = 0.125f * ARIA_LOG2E;
-    dim3 grid((Nq + 127) / 128, BH);
+    a.nqb = (Nq + 127) / 128;
+    a.T = a.nqb * BH;
+    const dim3 grid((a.T + 7) / 8 * 8);
     /* split the keys inside the workgroup when there are enough tiles for both halves
      * (S = 1296 self-attention: 21 tiles); short key sets (the 256 cross keys) run 4 waves */
     if ((Nk + KT - 1) / KT >= 8)

@@ -50,14 +50,9 @@ __device__ __forceinline__ void q8x4_to_h(uint32_t w, uint32_t &lo, uint32_t &hi
     hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias);
 }
 
-/* Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2):
- * workgroup g runs on XCD g % 8. Tile t = (g % 8) * ceil(T/8) + g / 8 gives each
- * XCD a contiguous run of tiles in M-major order, so an XCD's L2 holds a few
- * activation row panels and the weight panels instead of every activation row. */
-__device__ __forceinline__ int xcd_tile(int g, int T) {
-    const int per = (T + 7) >> 3;
-    return (g & 7) * per + (g >> 3);
-}
+/* xcd_tile (aria_dev.h) gives each XCD a contiguous run of tiles in M-major order, so an
+ * XCD's L2 holds a few activation row panels and the weight panels instead of every
+ * activation row. */
 
 /* Epilogue of one wave: its FM x FN blocks of 32x32 accumulators are staged through
  * LDS 32 rows at a time (fp32, rows padded by 16 B) and written as whole row segments:
