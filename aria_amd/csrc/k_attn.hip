@@ -259,12 +259,14 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
         /* S^T [64 keys x 32 queries] as two 32-key blocks */
         f32x16_t sc[2];
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
+        for (int r = 0; r < 16; r++) { sc[0][r] = 0.0f; sc[1][r] = 0.0f; }
+        /* the two 32-key blocks alternate: each chain's MFMA waits on its predecessor, and
+         * both fragments of a step arrive with one LDS wait */
 #pragma unroll
-            for (int r = 0; r < 16; r++) sc[kb][r] = 0.0f;
-#pragma unroll
-            for (int ds = 0; ds < 4; ds++)
-                sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ld_h8(K + koff[ds] + 32 * 64 * kb), qf[ds], sc[kb], 0, 0, 0);
+        for (int ds = 0; ds < 4; ds++) {
+            const half8_t k0 = ld_h8(K + koff[ds]), k1 = ld_h8(K + koff[ds] + 32 * 64);
+            sc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qf[ds], sc[0], 0, 0, 0);
+            sc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qf[ds], sc[1], 0, 0, 0);
         }
         if (kt0 + KT > a.Nk) {   /* ragged last tile: keys past the end get -inf */
 #pragma unroll
@@ -303,21 +305,27 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int kb = 0; kb < 2; kb++) {
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
+                /* the step's V^T fragments are requested before its exponentials, which then
+                 * cover the LDS latency */
+                const int s16 = 2 * kb + ks;
+                half8_t vf[2];
+#pragma unroll
+                for (int dt = 0; dt < 2; dt++) {
+                    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[dt] + 16 * 64 * s16));
+                    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[dt] + 16 * 64 * s16 + 8 * 64));
+                    const half4_t hl = __builtin_bit_cast(half4_t, lo), hh = __builtin_bit_cast(half4_t, hi);
+                    vf[dt] = half8_t{hl[0], hl[1], hl[2], hl[3], hh[0], hh[1], hh[2], hh[3]};
+                }
+                __builtin_amdgcn_sched_barrier(0);
                 float pv[8];
 #pragma unroll
                 for (int i = 0; i < 8; i++)
                     pv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][8 * ks + i], a.scale_log2, -m_use));
                 const half8_t pf = __builtin_bit_cast(half8_t, make_uint4(pack2h_rn(pv[0], pv[1]), pack2h_rn(pv[2], pv[3]),
                                                                           pack2h_rn(pv[4], pv[5]), pack2h_rn(pv[6], pv[7])));
-                const int s16 = 2 * kb + ks;
 #pragma unroll
-                for (int dt = 0; dt < 2; dt++) {
-                    const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[dt] + 16 * 64 * s16));
-                    const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t *)(V + voff[dt] + 16 * 64 * s16 + 8 * 64));
-                    const half4_t hl = __builtin_bit_cast(half4_t, lo), hh = __builtin_bit_cast(half4_t, hi);
-                    const half8_t vf = {hl[0], hl[1], hl[2], hl[3], hh[0], hh[1], hh[2], hh[3]};
-                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, oacc[dt], 0, 0, 0);
-                }
+                for (int dt = 0; dt < 2; dt++)
+                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[dt], pf, oacc[dt], 0, 0, 0);
                 /* row sum of the rounded P: exact fp16 products, fp32 accumulation */
 #pragma unroll
                 for (int e = 0; e < 4; e++)
