@@ -214,6 +214,23 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_wr(QArgs a, int NTN, int T)
                     acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w1, xf[ks][i], acc[i][1], 0, 0, 0);
                 }
             }
+        } else if constexpr (WT == ARIA_WQ4) {
+            /* FM >= 3, Q4: one MFMA step's fragments at a time, requested before that step's
+             * unpacking (+8 VGPRs; the Q8 kernels would cross 256 registers and lose their
+             * second wave per SIMD) */
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                half8_t xs[FM];
+#pragma unroll
+                for (int i = 0; i < FM; i++) xs[i] = *reinterpret_cast<const half8_t *>(&X[xoff(i * 32 + lrow, 4 * lh + ks)]);
+                __builtin_amdgcn_sched_barrier(0);
+                const half8_t w0 = wr_frag<WT>(ws, 0, ks, magic, f0), w1 = wr_frag<WT>(ws, 1, ks, magic, f1);
+#pragma unroll
+                for (int i = 0; i < FM; i++) {
+                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w0, xs[i], acc[i][0], 0, 0, 0);
+                    acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w1, xs[i], acc[i][1], 0, 0, 0);
+                }
+            }
         } else {
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
