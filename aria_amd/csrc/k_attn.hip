@@ -29,8 +29,9 @@
  * the accumulators are rarely rescaled; O / l does not depend on the reference chosen.
  * Workgroup: 4 waves x 32 queries = 128 queries of one (batch, head), or 8 waves when
  * the keys are split in two halves inside the workgroup (long key sets); K and V tiles
- * of 64 keys are staged key-major in LDS (swizzled, conflict-free) with register
- * prefetch of the next tile; the V^T operand is read with the gfx950 transpose load
+ * of 64 keys are staged key-major in LDS (swizzled, conflict-free) by LDS DMA
+ * (global_load_lds_dwordx4, no staging registers), the next tile's transfer running under
+ * the current tile's math; the V^T operand is read with the gfx950 transpose load
  * (ds_read_b64_tr_b16).
  */
 #include "aria_dev.h"
@@ -183,13 +184,19 @@ __device__ __forceinline__ uint32_t pack2h_rn(float x, float y) {
  * halves run the same number of loop trips, so every barrier is reached by all waves. */
 template <int KS>
 __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) void k_flash_attn(AttnArgs a) {
-    /* one buffer: K tiles [half][buf], then V tiles [half][buf], each KT x 64 fp16; after
-     * the key loop it holds the merge exchange (4 waves x 34 x 64 floats = 34.8 KB) */
-    __shared__ __attribute__((aligned(16))) uint16_t smem[2 * KS * 2 * KT * 64];
+    /* tile buffers, each [half][KT x 64] fp16, as four separate LDS objects: K and V tiles
+     * arrive by LDS DMA (global_load_lds), whose writes count on vmcnt, and the compiler only
+     * omits a vmcnt wait before a fragment read when the read provably targets another object
+     * than the pending DMA. After the key loop Kb0s + Kb1s hold the merge exchange (4 waves x
+     * 34 x 64 floats = 34.8 KB; the two objects are placed back to back, checked below). */
+    __shared__ __attribute__((aligned(16))) uint16_t Kb0s[KS * KT * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t Kb1s[KS * KT * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t Vb0s[KS * KT * 64];
+    __shared__ __attribute__((aligned(16))) uint16_t Vb1s[KS * KT * 64];
 
     const int half = KS == 1 ? 0 : (int)(threadIdx.x >> 8);
-    uint16_t *const Kb0 = smem + (half * 2) * (KT * 64), *const Kb1 = Kb0 + KT * 64;
-    uint16_t *const Vb0 = smem + (KS * 2 + half * 2) * (KT * 64), *const Vb1 = Vb0 + KT * 64;
+    uint16_t *const Kb0 = Kb0s + half * (KT * 64), *const Kb1 = Kb1s + half * (KT * 64);
+    uint16_t *const Vb0 = Vb0s + half * (KT * 64), *const Vb1 = Vb1s + half * (KT * 64);
     const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
     /* the query blocks of one (batch, head) run on one XCD, so its K and V are fetched
      * into that XCD's L2 once rather than into every XCD's */
@@ -210,25 +217,26 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int ds = 0; ds < 4; ds++) qf[ds] = ld_h8(Qh + (size_t)qi * 64 + 16 * ds + 8 * g);
     }
 
-    /* tile staging: slots t and t+256 = (key row s>>3, 16 B chunk s&7) of K and V; keys
-     * past Nk re-read the last key (their probabilities are exactly zero) */
-    uint4 rk0, rk1, rv0, rv1;
-    const int sl0 = tid, sl1 = tid + 256;
-    auto gload = [&](int kt0) {
-        const size_t off0 = (size_t)min(kt0 + (sl0 >> 3), a.Nk - 1) * 64 + 8 * (sl0 & 7);
-        const size_t off1 = (size_t)min(kt0 + (sl1 >> 3), a.Nk - 1) * 64 + 8 * (sl1 & 7);
-        rk0 = *reinterpret_cast<const uint4 *>(Kh + off0);
-        rv0 = *reinterpret_cast<const uint4 *>(Vh + off0);
-        rk1 = *reinterpret_cast<const uint4 *>(Kh + off1);
-        rv1 = *reinterpret_cast<const uint4 *>(Vh + off1);
+    /* tile staging by LDS DMA: instruction i of wave w (of this half) fills the 16 B slots
+     * p = 256 i + 64 w + lane of a K or V tile (key row p / 8, stored chunk p % 8), so each
+     * lane fetches the global chunk that the swizzle places there: K stores logical chunk c
+     * of row r at c ^ ((r >> 1) & 7), V at c ^ (((r >> 1) & 1) << 2). Keys past Nk re-read
+     * the last key (their probabilities are exactly zero). */
+    typedef __attribute__((address_space(3))) void lds_void_t;
+    const int wv = wave & 3;
+    auto dma = [&](int kt0, uint16_t *Kd, uint16_t *Vd) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int p = 256 * i + 64 * wv + lane, r = p >> 3, cp = p & 7;
+            const size_t row = (size_t)min(kt0 + r, a.Nk - 1) * 64;
+            const int ck = cp ^ ((r >> 1) & 7), cv = cp ^ (((r >> 1) & 1) << 2);
+            __builtin_amdgcn_global_load_lds(Kh + row + 8 * ck, (lds_void_t *)(Kd + (256 * i + 64 * wv) * 8), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Vh + row + 8 * cv, (lds_void_t *)(Vd + (256 * i + 64 * wv) * 8), 16, 0, 0);
+        }
     };
-    auto sstore = [&](int buf) {
-        uint16_t *Kd = buf ? Kb1 : Kb0, *Vd = buf ? Vb1 : Vb0;
-        *reinterpret_cast<uint4 *>(&Kd[k_off(sl0 >> 3, sl0 & 7)]) = rk0;
-        *reinterpret_cast<uint4 *>(&Vd[v_off(sl0 >> 3, 8 * (sl0 & 7))]) = rv0;
-        *reinterpret_cast<uint4 *>(&Kd[k_off(sl1 >> 3, sl1 & 7)]) = rk1;
-        *reinterpret_cast<uint4 *>(&Vd[v_off(sl1 >> 3, 8 * (sl1 & 7))]) = rv1;
-    };
+    /* the DMA writes into LDS complete on vmcnt; each wave waits for its own before the
+     * barrier that publishes the tile */
+    auto dma_wait = []() __attribute__((always_inline)) { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
     f32x16_t oacc[2];
 #pragma unroll
@@ -341,10 +349,8 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
     const int nt = max(0, min(niter, ntiles_all - tb));
     const int kbase = tb * KT;
     const uint16_t *K0 = Kb0, *V0 = Vb0, *K1 = Kb1, *V1 = Vb1;
-    if (nt > 0) {
-        gload(kbase);
-        sstore(0);
-    }
+    if (nt > 0) dma(kbase, Kb0, Vb0);
+    dma_wait();
     __syncthreads();
     /* two tiles per trip so each LDS buffer is a fixed address; buffer b^1 was last read
      * one tile earlier, before that tile's closing barrier. A wave whose 32 queries all lie
@@ -352,14 +358,14 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
      * meets the barriers; its products would never be stored. */
     const bool live = q0 < a.Nq;
     for (int t = 0; t < niter; t += 2) {
-        if (t + 1 < nt) gload(kbase + (t + 1) * KT);
+        if (t + 1 < nt) dma(kbase + (t + 1) * KT, Kb1, Vb1);
         if (live && t < nt) tile(kbase + t * KT, K0, V0);
-        if (t + 1 < nt) sstore(1);
+        dma_wait();
         __syncthreads();
         if (t + 1 < niter) {
-            if (t + 2 < nt) gload(kbase + (t + 2) * KT);
+            if (t + 2 < nt) dma(kbase + (t + 2) * KT, Kb0, Vb0);
             if (live && t + 1 < nt) tile(kbase + (t + 1) * KT, K1, V1);
-            if (t + 2 < nt) sstore(0);
+            dma_wait();
             __syncthreads();
         }
     }
@@ -368,24 +374,28 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
 
     if constexpr (KS == 2) {
         /* merge: the second half hands (O, l, m) to the first through LDS (the tile buffers
-         * are free after the last trip's barrier); per wave 64 lanes x 34 floats */
-        float *X = reinterpret_cast<float *>(smem) + wave * 34 * 64 + lane;
+         * are free after the last trip's barrier): per wave 64 lanes x 16 floats of each O
+         * block in Kb0s / Kb1s, l and m in Vb0s (each object holds 4 x 16 x 64 floats) */
+        static_assert(KS * KT * 64 * 2 >= 4 * 16 * 64 * 4, "merge exchange fits a tile buffer");
+        float *X0 = reinterpret_cast<float *>(Kb0s) + wave * 16 * 64 + lane;
+        float *X1 = reinterpret_cast<float *>(Kb1s) + wave * 16 * 64 + lane;
+        float *X2 = reinterpret_cast<float *>(Vb0s) + wave * 2 * 64 + lane;
         if (half == 1) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) { X[r * 64] = oacc[0][r]; X[(16 + r) * 64] = oacc[1][r]; }
-            X[32 * 64] = lrow;
-            X[33 * 64] = m_use;
+            for (int r = 0; r < 16; r++) { X0[r * 64] = oacc[0][r]; X1[r * 64] = oacc[1][r]; }
+            X2[0] = lrow;
+            X2[64] = m_use;
         }
         __syncthreads();
         if (half == 1) return;
-        const float m1 = X[33 * 64], l1 = X[32 * 64];
+        const float m1 = X2[64], l1 = X2[0];
         const float m = fmaxf(m_use, m1);   /* finite for a live wave (half 0 always has keys); a
                                              * wave past Nq returns below without storing */
         const float a0 = __builtin_amdgcn_exp2f(m_use - m), a1 = __builtin_amdgcn_exp2f(m1 - m);
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            oacc[0][r] = oacc[0][r] * a0 + X[r * 64] * a1;
-            oacc[1][r] = oacc[1][r] * a0 + X[(16 + r) * 64] * a1;
+            oacc[0][r] = oacc[0][r] * a0 + X0[r * 64] * a1;
+            oacc[1][r] = oacc[1][r] * a0 + X1[r * 64] * a1;
         }
         lrow = lrow * a0 + l1 * a1;
     }
