@@ -401,9 +401,16 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
     } else {
     if constexpr (WT != ARIA_WF16) {
         /* weights-in-registers kernel: explicit tiles 9..12 (BM = 32 * (tiles - 8)), or the pick */
-        const int fm = (tiles > NCFG) ? tiles - NCFG : (tiles == 0 ? pick_wr(a.M, a.N, a.K) : 0);
+        int fm = (tiles > NCFG) ? tiles - NCFG : (tiles == 0 ? pick_wr(a.M, a.N, a.K) : 0);
+        /* Q8 with N and K <= 1024 (the DiT's sa_out / ca_out): 64 x 64 LDS-operand tiles, 2.5
+         * workgroups per CU, measured 8 % faster than the weights-in-registers pick */
+        if (tiles == 0 && WT == ARIA_WQ8 && a.N <= 1024 && a.K <= 1024 && a.epi.mode != ARIA_EPI_HEADS) fm = 0;
         const bool wr_ok = a.K % 64 == 0 && (!a.gelu || a.epi.mode == ARIA_EPI_STORE);
         if (fm > 0 && wr_ok) return qgemm_wr_launch(a, WT, fm, s);
+        if (tiles == 0 && fm == 0 && WT == ARIA_WQ8 && a.N <= 1024 && a.K <= 1024 && a.epi.mode != ARIA_EPI_HEADS) {
+            launch_cfg<C8, WT, AF16>(a, s);
+            return hipGetLastError();
+        }
     }
     int c = (tiles >= 1 && tiles <= NCFG) ? tiles - 1 : pick_tiles(a.M, a.N, a.epi.mode == ARIA_EPI_HEADS);
     if (a.epi.mode == ARIA_EPI_HEADS && cfg_fn[c] < 2) c = pick_tiles(a.M, a.N, true);
