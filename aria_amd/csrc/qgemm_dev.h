@@ -125,12 +125,13 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
         return g;
     };
     bool gpre = false;
-    int blo = 0;
+    int blo = 0, bnd = 0;                       /* bnd: first row of batch blo + 1 */
     float4 gs0 = make_float4(0.f, 0.f, 0.f, 0.f), gs1 = gs0;
     if constexpr (MODE == ARIA_EPI_GATE_RES) {
         const int rpb = a.epi.rows_per_batch;
         const int mlast = min(mw + 32 * FM - 1, a.M - 1);
         blo = min(mw, a.M - 1) / rpb;
+        bnd = (blo + 1) * rpb;
         gpre = mlast / rpb <= blo + 1;
         if (gpre) {
             const int nbc = col_ok ? nb : 0, bhi = min(blo + 1, (a.M - 1) / rpb);
@@ -160,6 +161,17 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
         rope = kind != 2 && e.rot > 0 && e.cos_t && d0 < e.rot;
         first = d0 < rh;
         i0 = first ? d0 : d0 - rh;
+    }
+    /* HEADS: (batch, position) of this lane's current row, m = hb * S + hs. The rows a lane
+     * visits rise by RPI per store (and per 32-row group, NIT * RPI = 32), so the pair is
+     * advanced by (RPI / S, RPI % S) with one carry instead of a division per row. */
+    int hb = 0, hs = 0, hq = 0, hr = 0;
+    if constexpr (MODE == ARIA_EPI_HEADS) {
+        const int S = e.rows_per_batch, m0 = mw + erow;
+        hb = m0 / S;
+        hs = m0 - hb * S;
+        hq = RPI / S;
+        hr = RPI - hq * S;
     }
 #pragma unroll
     for (int i = 0; i < FM; i++) {
@@ -229,7 +241,7 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
                 if (MODE == ARIA_EPI_GATE_RES) {
                     /* y += v * sigmoid(1 - gate): the rounding order of k_gate_residual */
                     float4 sg;
-                    if (gpre) sg = (m / e.rows_per_batch == blo) ? gs0 : gs1;
+                    if (gpre) sg = (m < bnd) ? gs0 : gs1;
                     else sg = make_float4(gate_sig_f(g2[it].x), gate_sig_f(g2[it].y), gate_sig_f(g2[it].z), gate_sig_f(g2[it].w));
                     o = make_float4(rr[it].x + v[it][0] * sg.x, rr[it].y + v[it][1] * sg.y,
                                     rr[it].z + v[it][2] * sg.z, rr[it].w + v[it][3] * sg.w);
@@ -242,13 +254,18 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
         } else {   /* HEADS */
             const int S = e.rows_per_batch;
             float4 cs[NIT], sn[NIT];
+            int sb[NIT], sp[NIT];
 #pragma unroll
             for (int it = 0; it < NIT; it++) {
+                sb[it] = hb;
+                sp[it] = hs;   /* hs < S: the table row is in range past M too */
                 if (rope) {
-                    const int s = min(mrow[it], a.M - 1) % S;
-                    cs[it] = *reinterpret_cast<const float4 *>(e.cos_t + (size_t)s * rh + i0);
-                    sn[it] = *reinterpret_cast<const float4 *>(e.sin_t + (size_t)s * rh + i0);
+                    cs[it] = *reinterpret_cast<const float4 *>(e.cos_t + (size_t)hs * rh + i0);
+                    sn[it] = *reinterpret_cast<const float4 *>(e.sin_t + (size_t)hs * rh + i0);
                 }
+                hs += hr;
+                hb += hq;
+                if (hs >= S) { hs -= S; hb++; }
             }
 #pragma unroll
             for (int it = 0; it < NIT; it++) {
@@ -278,8 +295,7 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
                     }
                 }
                 if (m < a.M && col_ok) {
-                    const int s = m % S, b = m / S;
-                    uint16_t *d = dsec + (((size_t)b * e.heads + hh) * S + s) * 64 + 4 * l16;
+                    uint16_t *d = dsec + (((size_t)sb[it] * e.heads + hh) * S + sp[it]) * 64 + 4 * l16;
                     *reinterpret_cast<uint2 *>(d) = make_uint2(pack2h(w4[0], w4[1]), pack2h(w4[2], w4[3]));
                 }
             }
