@@ -91,6 +91,10 @@ SIGNATURES = {
     "aria_hip_q8_dequant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
     "aria_hip_q4_dequant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
     "aria_hip_qlinear_dev": (_i, [_P, _i, _P, _i, _i, _P, _P, _P, _i, _i, _i, _P]),
+    "aria_hip_quant_act_q8_dev": (_i, [_P, _P, _P, _i, _i, _i, _P]),
+    "aria_hip_gemm_i8_dev": (_i, [_P, _i, _P, _P, _P, _P, _P, _i, _i, _i, _P]),
+    "aria_hip_q8a8_ws_bytes": (_sz, [_i, _i]),
+    "aria_hip_linear_q8a8_dev": (_i, [_P, _P, _i, _P, _P, _P, _i, _i, _i, _P, _P]),
     "aria_hip_qlinear_ex_dev": (_i, [_P, _i, _P, _i, _i, _P, _P, _P, _i, _i, _i, _i, _P]),
     "aria_hip_linear_q8_dev": (_i, [_P, _P, _P, _P, _P, _i, _i, _i, _P]),
     "aria_hip_linear_q4_dev": (_i, [_P, _P, _P, _P, _P, _i, _i, _i, _P]),
@@ -124,6 +128,7 @@ SIGNATURES = {
     "aria_cuda_dec_medium_forward": (None, [_P, _P, _P, _i]),
     # include/aria_hip.h: host-pointer forms
     "aria_hip_linear_q8": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
+    "aria_hip_linear_q8a8": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
     "aria_hip_linear_q4": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
     "aria_hip_q8_quant": (_i, [_P, _P, _P, _i, _i]),
     "aria_hip_q4_quant": (_i, [_P, _P, _P, _i, _i]),

@@ -506,6 +506,38 @@ int aria_hip_linear_q4_dev(float *dy, const float *dx, const uint8_t *dq, const 
     return aria_hip_qlinear_dev(dy, 0, dx, 0, ARIA_WQ4, dq, dscale, db, M, K, N, stream);
 }
 
+/* W8A8 (k_gemm_i8.hip) */
+int aria_hip_quant_act_q8_dev(int8_t *dxq, float *dsx, const void *dx, int x_f16, int M, int K, void *stream) {
+    ENSURE();
+    REQ(M >= 0 && K > 0 && (M == 0 || (dxq && dsx && dx)));
+    REQ(K % 4 || (((uintptr_t)dxq & 3u) == 0 && ((uintptr_t)dx & (x_f16 ? 7u : 15u)) == 0));
+    KCK(aria_k_quant_act_q8(dxq, dsx, dx, x_f16, M, K, pick(stream)), "k_quant_act_q8");
+    return 0;
+}
+int aria_hip_gemm_i8_dev(void *dy, int y_f16, const int8_t *dxq, const float *dsx, const int8_t *dq,
+                         const float *dscale, const float *db, int M, int K, int N, void *stream) {
+    ENSURE();
+    REQ(M >= 0 && K > 0 && N >= 0 && (M == 0 || N == 0 || (dy && dxq && dsx && dq && dscale)));
+    KCK(aria_k_gemm_i8(dy, y_f16, dxq, dsx, dq, dscale, db, M, K, N, 0, NULL, pick(stream)), "k_gemm_i8");
+    return 0;
+}
+size_t aria_hip_q8a8_ws_bytes(int M, int K) {
+    if (M <= 0 || K <= 0) return 0;
+    return (((size_t)M * K + 255) & ~(size_t)255) + (size_t)M * sizeof(float);
+}
+int aria_hip_linear_q8a8_dev(float *dy, const void *dx, int x_f16, const int8_t *dq, const float *dscale,
+                             const float *db, int M, int K, int N, void *dws, void *stream) {
+    ENSURE();
+    REQ(M >= 0 && K > 0 && N >= 0);
+    if (M == 0 || N == 0) return 0;
+    REQ(dy && dx && dq && dscale && dws && ((uintptr_t)dws & 255u) == 0);
+    int8_t *xq = (int8_t *)dws;
+    float *sx = (float *)(void *)((char *)dws + (((size_t)M * K + 255) & ~(size_t)255));
+    int r = aria_hip_quant_act_q8_dev(xq, sx, dx, x_f16, M, K, stream);
+    if (r) return r;
+    return aria_hip_gemm_i8_dev(dy, 0, xq, sx, dq, dscale, db, M, K, N, stream);
+}
+
 /* ------------------------------------------------------------------------- */
 /* host-pointer forms (aria_hip.h) - one synchronous staged call each        */
 /* ------------------------------------------------------------------------- */
@@ -554,6 +586,23 @@ int aria_hip_linear_q8(float *y, const float *x, const int8_t *q, const float *s
 int aria_hip_linear_q4(float *y, const float *x, const uint8_t *q, const float *scale, const float *b, int M,
                        int K, int N) {
     return host_qlinear(y, x, ARIA_WQ4, q, scale, b, M, K, N);
+}
+int aria_hip_linear_q8a8(float *y, const float *x, const int8_t *q, const float *scale, const float *b, int M,
+                         int K, int N) {
+    HOST_BEGIN();
+    REQ(M >= 0 && K > 0 && N >= 0 && y && x && q && scale);
+    if (M == 0 || N == 0) return 0;
+    float *dx = st_in(&st_, x, FB((size_t)M * K));
+    void *dq = st_in(&st_, q, (size_t)N * K);
+    float *ds = st_in(&st_, scale, FB(N));
+    float *db = st_in(&st_, b, FB(N));
+    float *dy = st_alloc(&st_, FB((size_t)M * N));
+    int8_t *xq = st_alloc(&st_, (size_t)M * K);
+    float *sx = st_alloc(&st_, FB(M));
+    if (!st_.err) st_kernel(&st_, aria_k_quant_act_q8(xq, sx, dx, 0, M, K, g_stream), "k_quant_act_q8");
+    if (!st_.err) st_kernel(&st_, aria_k_gemm_i8(dy, 0, xq, sx, dq, ds, db, M, K, N, 0, NULL, g_stream), "k_gemm_i8");
+    st_out(&st_, y, dy, FB((size_t)M * N));
+    HOST_END();
 }
 
 

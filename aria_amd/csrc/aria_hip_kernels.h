@@ -90,7 +90,7 @@ hipError_t aria_k_q4_dequant(float *W, const uint8_t *q, const float *scale, int
  * wtype: ARIA_WQ8 (q int8 [N,K], scale [N]), ARIA_WQ4 (q u8 [N,ceil(K/2)], scale
  * [N, 2*ceil(K/32)] as [min, step] pairs), ARIA_WF16 (q = fp16 W [N,K], scale unused).
  * x is fp32 or fp16 (x_f16), y fp32 or fp16 (y_f16). */
-enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2 };
+enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2, ARIA_WI8 = 3 };
 /* Fused epilogues, applied to v = acc * scale (+ bias) (GELU'd when gelu != 0):
  *   STORE     y = v (fp32 or fp16)
  *   GATE_RES  y = y + v * sigmoid(1 - g), g = gate[b * gate_bs + col]
@@ -127,6 +127,23 @@ hipError_t aria_k_qgemm_t(void *y, int y_f16, const void *x, int x_f16, int wtyp
 hipError_t aria_k_qgemm_e(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                           const float *scale, const float *bias, int M, int K, int N, int tiles,
                           int gelu, const aria_qgemm_epi *epi, hipStream_t s);
+
+/* W8A8 (k_gemm_i8.hip), the reference's gemm_w8a8 (src/aria_cuda.cu:934-990) and
+ * aria_linear_q8a8 (src/aria_quant.c:253-345).
+ * aria_k_quant_act_q8: per row, amax = max |x|, sx[m] = amax / 127, xq = clamp(rint(x * 127 /
+ *   amax), -127, 127) (all zero when amax == 0); x fp32 or fp16 (x_f16) [M, K].
+ * aria_k_gemm_i8: y = (float)(xq . q) * sx[m] * scale[n] (+ bias[n], else + 0.0f): exact int32
+ *   dot products on the int8 MFMA, the two multiplies rounded in that order, then the fused
+ *   epilogue (epi NULL = STORE; gelu as in aria_k_qgemm_e). K % 64 == 0 with 16-byte aligned
+ *   rows runs the MFMA kernel; other shapes a SIMT kernel (STORE only, no GELU). */
+hipError_t aria_k_quant_act_q8(int8_t *xq, float *sx, const void *x, int x_f16, int M, int K, hipStream_t s);
+hipError_t aria_k_gemm_i8(void *y, int y_f16, const int8_t *xq, const float *sx, const int8_t *q,
+                          const float *scale, const float *bias, int M, int K, int N, int gelu,
+                          const aria_qgemm_epi *epi, hipStream_t s);
+/* the same with the tile height fixed: fm = 1..4 (32 fm rows x 256 columns), 0 = picked */
+hipError_t aria_k_gemm_i8_t(void *y, int y_f16, const int8_t *xq, const float *sx, const int8_t *q,
+                            const float *scale, const float *bias, int M, int K, int N, int fm, int gelu,
+                            const aria_qgemm_epi *epi, hipStream_t s);
 
 /* Attention (k_attn.hip). Head preparation: src [B*S, ld] fp32 holds nsec sections of
  * H*64 columns; kind[i] = 0 (q: RMSNorm w[i] + RoPE), 1 (k: same), 2 (v: copy); each

@@ -435,6 +435,7 @@ extern "C" hipError_t aria_k_qgemm_e(void *y, int y_f16, const void *x, int x_f1
     QArgs a;
     a.y = y; a.x = x; a.q = q; a.scale = scale; a.bias = bias;
     a.M = M; a.K = K; a.N = N; a.y_f16 = y_f16; a.nblk = (K + 31) / 32; a.gelu = gelu;
+    a.xscale = nullptr;
     if (epi) a.epi = *epi;
     else { memset(&a.epi, 0, sizeof a.epi); a.epi.mode = ARIA_EPI_STORE; }
     if (a.epi.mode == ARIA_EPI_HEADS) {

@@ -106,15 +106,6 @@ __device__ __forceinline__ half8_t wr_frag(const WRegs<WT> &s, int j, int ks, ui
     return __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-/* f(IC<0>{}), ..., f(IC<N-1>{}) */
-template <int N, int I = 0, class Fn>
-__device__ __forceinline__ void static_for(Fn &&f) {
-    if constexpr (I < N) {
-        f(IC<I>{});
-        static_for<N, I + 1>(f);
-    }
-}
-
 template <int WT, int FM, int MINB, int MODE, bool GELU, int DP = (WT == ARIA_WQ8 && FM >= 3 ? 3 : 2)>
 __global__ __launch_bounds__(256, MINB) void k_qgemm_wr(QArgs a, int NTN, int T) {
     constexpr int FN = 2, BM = 32 * FM, BN = 256;

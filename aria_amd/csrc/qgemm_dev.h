@@ -15,6 +15,14 @@
 
 template <int I>
 using IC = std::integral_constant<int, I>;
+/* f(IC<0>{}), ..., f(IC<N-1>{}) */
+template <int N, int I = 0, class Fn>
+__device__ __forceinline__ void static_for(Fn &&f) {
+    if constexpr (I < N) {
+        f(IC<I>{});
+        static_for<N, I + 1>(f);
+    }
+}
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -31,6 +39,7 @@ struct QArgs {
     int y_f16;
     int nblk;
     int gelu;   /* epilogue: y = gelu_tanh(acc*scale + b) (the config FFN's activation) */
+    const float *xscale;   /* ARIA_WI8: per-row activation scale sx[M] (unused otherwise) */
     aria_qgemm_epi epi;
 };
 
@@ -72,8 +81,8 @@ __device__ __forceinline__ void q8x4_to_h(uint32_t w, uint32_t &lo, uint32_t &hi
  * head-aligned); the arithmetic is k_qkv_prep's (k_attn.hip): RMS statistic in fp32
  * over the head, (x * inv) * w, then rotate-half RoPE over the first rot dims. */
 #define EPI_ANY (-1)
-template <int FM, int FN, int WT, int MODE, bool GELU = false>
-__device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN], float *E, int lane, int mw, int nw) {
+template <int FM, int FN, int WT, int MODE, bool GELU = false, typename AccT = f32x16_t>
+__device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], float *E, int lane, int mw, int nw) {
     constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
     constexpr int CW = 32 * FN;                 /* columns per wave */
     constexpr int LPR = CW / 4;                 /* lanes per row (16 B each) */
@@ -110,8 +119,9 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
     const bool col_ok = nb < a.N;
     float4 sc = make_float4(1.0f, 1.0f, 1.0f, 1.0f), bb = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
     if (col_ok) {
-        if (WT == ARIA_WQ8) sc = *reinterpret_cast<const float4 *>(a.scale + nb);
+        if (WT == ARIA_WQ8 || WT == ARIA_WI8) sc = *reinterpret_cast<const float4 *>(a.scale + nb);
         if (a.bias) bb = *reinterpret_cast<const float4 *>(a.bias + nb);
+        else if (WT == ARIA_WI8) bb = make_float4(0.0f, 0.0f, 0.0f, 0.0f);   /* the reference adds 0.0f */
     }
     /* GATE_RES: the gate depends on (batch, column) only, so sigmoid(1 - gate) is formed
      * once per lane for the (at most two) batches this wave's rows span; a tile spanning
@@ -181,7 +191,8 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
             for (int g = 0; g < 4; g++)
                 *reinterpret_cast<float4 *>(reinterpret_cast<char *>(E) + lrow * EPI_STRIDE +
                                             (j * 32 + 8 * g + 4 * lh) * 4) =
-                    make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+                    make_float4((float)acc[i][j][4 * g], (float)acc[i][j][4 * g + 1], (float)acc[i][j][4 * g + 2],
+                                (float)acc[i][j][4 * g + 3]);   /* int32 (W8A8): v_cvt_f32_i32, nearest even */
         __builtin_amdgcn_wave_barrier();
         float v[NIT][4];
         int mrow[NIT];
@@ -193,9 +204,12 @@ __device__ __forceinline__ void epilogue(const QArgs &a, f32x16_t (&acc)[FM][FN]
                                                                 r * EPI_STRIDE + ecol * 4);
             v[it][0] = v4.x; v[it][1] = v4.y; v[it][2] = v4.z; v[it][3] = v4.w;
             const float scv[4] = {sc.x, sc.y, sc.z, sc.w}, bv[4] = {bb.x, bb.y, bb.z, bb.w};
+            float xsv = 1.0f;   /* W8A8: (float)acc * sx[m] * scale[n], in that order */
+            if constexpr (WT == ARIA_WI8) xsv = a.xscale[min(mrow[it], a.M - 1)];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                if (WT == ARIA_WQ8) v[it][q] = v[it][q] * scv[q];
+                if (WT == ARIA_WI8) v[it][q] = v[it][q] * xsv;
+                if (WT == ARIA_WQ8 || WT == ARIA_WI8) v[it][q] = v[it][q] * scv[q];
                 v[it][q] = v[it][q] + bv[q];
                 if constexpr (GELU) v[it][q] = gelu_tanh_f(v[it][q]);
             }

@@ -236,6 +236,18 @@ def linear_q4(x, q, s, b=None):
     return y
 
 
+def linear_q8a8(x, q, s, b=None):
+    """aria_linear_q8a8 (src/aria_quant.h:50): per-row int8 activations, exact int32 dot
+    products on the int8 MFMA, y = acc * sx[m] * s[n] + b (bit-identical to the reference)."""
+    x = _f32(x); b = _f32(b)
+    M, K = x.shape
+    N = q.shape[0]
+    y = np.empty((M, N), np.float32)
+    check(lib().aria_hip_linear_q8a8(_p(y), _p(x), _p(np.ascontiguousarray(q)), _p(np.ascontiguousarray(s)),
+                                     _p(b), M, K, N), "aria_hip_linear_q8a8")
+    return y
+
+
 def q8_dequant(q, s):
     N, K = q.shape
     W = np.empty((N, K), np.float32)

@@ -149,6 +149,30 @@ int aria_hip_linear_q8_dev(float *dy, const float *dx, const int8_t *dq, const f
 int aria_hip_linear_q4_dev(float *dy, const float *dx, const uint8_t *dq, const float *dscale,
                            const float *db, int M, int K, int N, void *stream);
 
+/* ---- W8A8: int8 activations x int8 weights on the int8 MFMA ----
+ * Replaces the reference's gemm_w8a8 / gemm_w8a8_h (src/aria_cuda.cu:934-1004: per-token
+ * activation quantisation k_quant_act_q8(_h), int8 IMMA GEMM into int32, dequant k_deq_i32)
+ * with the numbers of aria_linear_q8a8 (src/aria_quant.h:47-51, src/aria_quant.c:253-345),
+ * bit for bit. */
+/* Per-row symmetric int8 activations: sx[m] = amax / 127 (amax = max |x[m,:]|),
+ * dxq[m,k] = clamp(rint(x * 127 / amax), -127, 127), all zero when amax == 0. dx is
+ * fp32 or fp16 (x_f16) [M, K]; dxq [M, K] int8, dsx [M]. */
+int aria_hip_quant_act_q8_dev(int8_t *dxq, float *dsx, const void *dx, int x_f16, int M, int K,
+                              void *stream);
+/* dy[m,n] = (float)(sum_k dxq[m,k] dq[n,k]) * dsx[m] * dscale[n] (+ db[n], else + 0.0f),
+ * exact int32 sums, fp32 (or fp16 with y_f16) output. dq / dscale are the Q8 weight
+ * (aria_q8_quant layout). */
+int aria_hip_gemm_i8_dev(void *dy, int y_f16, const int8_t *dxq, const float *dsx, const int8_t *dq,
+                         const float *dscale, const float *db, int M, int K, int N, void *stream);
+/* Both steps, as aria_linear_q8a8 on device data: dws is caller workspace of at least
+ * aria_hip_q8a8_ws_bytes(M, K) bytes (the int8 rows and their scales). */
+size_t aria_hip_q8a8_ws_bytes(int M, int K);
+int aria_hip_linear_q8a8_dev(float *dy, const void *dx, int x_f16, const int8_t *dq, const float *dscale,
+                             const float *db, int M, int K, int N, void *dws, void *stream);
+/* Host-pointer form with the reference's signature (src/aria_quant.h:50). */
+int aria_hip_linear_q8a8(float *y, const float *x, const int8_t *q, const float *scale, const float *b,
+                         int M, int K, int N);
+
 /* ---- attention (the DiT's, head dim 64) ----
  * Head preparation, replacing extract_heads + q/k RMSNorm + RoPE of the block
  * (src/aria_sa3_dit.c:183-194, 222-226): dsrc [B*S, ld] fp32 holds nsec sections of

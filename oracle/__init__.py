@@ -142,6 +142,23 @@ class _Lib:
                               _i(M), _i(K), _i(N))
         return y
 
+    def linear_q8a8(self, x, q, s, b=None):
+        _chk(x, np.float32)
+        M, K = x.shape
+        N = q.shape[0]
+        y = np.empty((M, N), np.float32)
+        self._fn("linear_q8a8")(_fp(y), _fp(x), q.ctypes.data_as(_I8), _fp(s), _fp(b),
+                                _i(M), _i(K), _i(N))
+        return y
+
+    def quant_act_q8(self, x):
+        """port only (the reference quantises inside aria_linear_q8a8)"""
+        _chk(x, np.float32)
+        M, K = x.shape
+        xq = np.empty((M, K), np.int8); sx = np.empty(M, np.float32)
+        self._fn("quant_act_q8")(xq.ctypes.data_as(_I8), _fp(sx), _fp(x), _i(M), _i(K))
+        return xq, sx
+
     def linear_q4(self, x, q, s, b=None):
         _chk(x, np.float32)
         M, K = x.shape

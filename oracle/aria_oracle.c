@@ -18,6 +18,10 @@
  *   or_q8/q4_quant    bit-exact vs the compiled reference aria_q8_quant/aria_q4_quant;
  *                     closed forms (zero row, constant block, +-amax -> +-127, odd-K pad nibble).
  *   or_linear_q8/q4   vs reference aria_linear_q8/q4; identity-weight brute force in double.
+ *   or_quant_act_q8 / or_linear_q8a8  bit-exact vs the compiled reference aria_linear_q8a8
+ *                     on the reference's own W8A8 shapes (tests/test_quant.c:141-170);
+ *                     closed forms (row max -> +-127, zero row -> 0, int64 brute force of
+ *                     the dot products, one-hot weights pick one column).
  *   or_linear         vs an independent float64 numpy matmul; KAT tests/test_ops.c:53-63.
  *   or_attention      vs compiled reference aria_attention; uniform-score closed form.
  *   or_pingpong       tc=tn=0 identity; vs numpy float32 step-by-step rounding.
@@ -337,6 +341,51 @@ void or_linear_q8(float *y, const float *x, const int8_t *q, const float *scale,
             y[(size_t)m * N + n] = s + (b ? b[n] : 0.0f);
         }
     }
+}
+
+/* W8A8 activation quantisation, the row loop of src/aria_quant.c:258-270: amax = max |x|
+ * (a strict > scan from 0), sx = amax / 127, xq = clamp(lrintf(x * (127 / amax)), -127, 127),
+ * all zero when amax == 0. */
+void or_quant_act_q8(int8_t *xq, float *sx, const float *x, int M, int K) {
+    for (int m = 0; m < M; m++) {
+        const float *xr = x + (size_t)m * K;
+        int8_t *qr = xq + (size_t)m * K;
+        float amax = 0.0f;
+        for (int k = 0; k < K; k++) { float a = fabsf(xr[k]); if (a > amax) amax = a; }
+        sx[m] = amax / 127.0f;
+        if (amax > 0.0f) {
+            float inv = 127.0f / amax;
+            for (int k = 0; k < K; k++) {
+                long v = lrintf(xr[k] * inv);
+                qr[k] = (int8_t)(v < -127 ? -127 : (v > 127 ? 127 : v));
+            }
+        } else {
+            memset(qr, 0, (size_t)K);
+        }
+    }
+}
+
+/* W8A8 GEMM, the scalar branch of src/aria_quant.c:272-345: acc = sum_k xq*q in int32
+ * (exact), y = (float)acc * sx[m] * scale[n] + (b ? b[n] : 0.0f), left to right. */
+void or_linear_q8a8(float *y, const float *x, const int8_t *q, const float *scale,
+                    const float *b, int M, int K, int N) {
+    int8_t *xq = (int8_t *)malloc((size_t)M * K + 1);
+    float *sx = (float *)malloc((size_t)M * sizeof(float) + 4);
+    if (!xq || !sx) { free(xq); free(sx); return; }
+    or_quant_act_q8(xq, sx, x, M, K);
+    for (int m = 0; m < M; m++) {
+        const int8_t *xr = xq + (size_t)m * K;
+        for (int n = 0; n < N; n++) {
+            const int8_t *qn = q + (size_t)n * K;
+            int32_t acc = 0;
+            for (int k = 0; k < K; k++) acc += (int32_t)xr[k] * qn[k];
+            float v = (float)acc * sx[m];
+            v = v * scale[n];
+            y[(size_t)m * N + n] = v + (b ? b[n] : 0.0f);
+        }
+    }
+    free(xq);
+    free(sx);
 }
 
 /* Q4 dequant-on-use GEMM, src/aria_quant.c:469-538 (its x86 build is this scalar

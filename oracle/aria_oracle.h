@@ -63,6 +63,9 @@ void or_q8_dequant(float *W, const int8_t *q, const float *scale, int N, int K);
 void or_q4_dequant(float *W, const uint8_t *q, const float *scale, int N, int K);
 void or_linear_q8(float *y, const float *x, const int8_t *q, const float *scale,
                   const float *b, int M, int K, int N);
+void or_quant_act_q8(int8_t *xq, float *sx, const float *x, int M, int K);
+void or_linear_q8a8(float *y, const float *x, const int8_t *q, const float *scale,
+                    const float *b, int M, int K, int N);
 void or_linear_q4(float *y, const float *x, const uint8_t *q, const float *scale,
                   const float *b, int M, int K, int N);
 

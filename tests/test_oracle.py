@@ -233,6 +233,56 @@ def test_quant_closed_forms(port):
     assert s8[0] == 1.0 and list(q8[0, :4]) == [127, 2, 4, -2]
 
 
+# the reference's W8A8 exactness shapes (tests/test_quant.c:146), (M, K, N)
+W8A8_SHAPES = [(1, 32, 1), (3, 64, 2), (4, 96, 3), (5, 100, 4), (7, 1030, 7), (9, 1024, 13), (12, 256, 6)]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def test_w8a8_vs_reference(port, R):
+    """or_linear_q8a8 against the compiled reference aria_linear_q8a8, bit for bit (the
+    reference itself checks its AVX2 path against a scalar loop on these shapes)."""
+    r = rng(31)
+    for M, K, N in W8A8_SHAPES + [(17, 1024, 40), (6, 4096, 9)]:
+        W = randn(r, (N, K), 0.1); x = randn(r, (M, K)); b = randn(r, N)
+        x[M // 2] = 0.0                                    # amax == 0 row
+        q, s = port.q8_quant(W)
+        for bias in (b, None):
+            assert np.array_equal(_bits(port.linear_q8a8(x, q, s, bias)), _bits(R.linear_q8a8(x, q, s, bias))), (M, K, N)
+
+
+def test_w8a8_closed_forms(port):
+    # quantiser: ties to even (lrintf), the row maximum to +-127, a zero row to 0 / sx 0
+    x = np.zeros((3, 8), np.float32)
+    x[0, :6] = [127.0, 0.5, 1.5, 2.5, -0.5, -126.5]
+    x[2, :3] = [-3.0, 1.0, 2.0]
+    xq, sx = port.quant_act_q8(x)
+    assert sx[0] == np.float32(1.0) and list(xq[0, :6]) == [127, 0, 2, 2, 0, -126]
+    assert sx[1] == 0.0 and np.all(xq[1] == 0)
+    assert sx[2] == np.float32(3.0) / np.float32(127.0) and xq[2, 0] == -127
+    assert list(xq[2, 1:3]) == [int(np.rint(np.float32(1.0) * (np.float32(127.0) / np.float32(3.0)))),
+                                int(np.rint(np.float32(2.0) * (np.float32(127.0) / np.float32(3.0))))]
+    # GEMM: the int32 sums against an int64 brute force; one-hot weights pick one column
+    r = rng(33)
+    M, K, N = 9, 200, 11
+    x = randn(r, (M, K)); W = randn(r, (N, K), 0.1); b = randn(r, N)
+    q, s = port.q8_quant(W)
+    xq, sx = port.quant_act_q8(x)
+    acc = xq.astype(np.int64) @ q.astype(np.int64).T
+    want = (acc.astype(np.float32) * sx[:, None]) * s[None, :] + b[None, :]
+    assert np.array_equal(_bits(port.linear_q8a8(x, q, s, b)), _bits(want))
+    Wo = np.zeros((N, K), np.float32)
+    cols = (np.arange(N) * 17) % K
+    Wo[np.arange(N), cols] = 2.0
+    qo, so = port.q8_quant(Wo)
+    assert np.all(qo[np.arange(N), cols] == 127)
+    y = port.linear_q8a8(x, qo, so)
+    want = (xq[:, cols].astype(np.float32) * np.float32(127) * sx[:, None]) * so[None, :]
+    assert np.array_equal(_bits(y), _bits(want + np.float32(0.0)))
+
+
 def test_quant_gemm_brute_force(port):
     """Dequant-on-use GEMMs vs float64 x @ dequant(W)^T: pins operand order and scale use."""
     r = rng(10)
