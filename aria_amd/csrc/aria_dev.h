@@ -138,6 +138,20 @@ __device__ __forceinline__ uint16_t f2h_bits(float v) {
     return __builtin_bit_cast(uint16_t, h);
 }
 
+/* W8A8 activation quantisation of four values (src/aria_quant.c:264-266): rint (ties to
+ * even, as lrintf in the default rounding mode) of v * inv, clamped to [-127, 127], packed
+ * as four int8 in one word (element 0 in the low byte) */
+__device__ __forceinline__ uint32_t q8_pack4(float4 v, float inv) {
+    const float f[4] = {v.x * inv, v.y * inv, v.z * inv, v.w * inv};
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = min(max((int)__builtin_rintf(f[i]), -127), 127);
+        w |= (uint32_t)(q & 0xFF) << (8 * i);
+    }
+    return w;
+}
+
 /* non-temporal 128-bit load/store of a float4 (streamed-once data) */
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 ld_nt(const float4 *p) {

@@ -184,7 +184,11 @@ int aria_cuda_recommended(void) {
     return strncmp(g_prop.gcnArchName, "gfx950", 6) == 0 || strncmp(g_prop.gcnArchName, "gfx942", 6) == 0;
 }
 
-int aria_cuda_int8_tc(void) { return 0; }
+/* the W8A8 path (k_gemm_i8.hip) runs on gfx950's int8 MFMA (v_mfma_i32_32x32x32_i8) */
+int aria_cuda_int8_tc(void) {
+    if (ensure()) return 0;
+    return strncmp(g_prop.gcnArchName, "gfx950", 6) == 0;
+}
 
 void aria_cuda_device_info(char *buf, size_t buflen) {
     if (!buf || !buflen) return;

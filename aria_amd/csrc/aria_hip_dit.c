@@ -43,6 +43,7 @@ typedef struct {
 
 struct aria_hip_dit_block {
     int dim, H, hd, inner, ffn, dim_ctx, ffrows;
+    int w8;   /* ARIA_Q8A8: every Q8 projection runs on int8 activations (W8A8) */
     aria_dtype prec;
     float *pre_norm, *cross_norm, *ff_norm, *sa_q_norm, *sa_k_norm, *ca_q_norm, *ca_k_norm;
     float *ff_in_b, *ff_out_b, *tssg;
@@ -127,11 +128,17 @@ aria_hip_dit_block *aria_hip_dit_block_create(const aria_dit_block_w *w, int dim
                            dim, num_heads, head_dim, inner, dim_ctx);
         return NULL;
     }
+    if (precision == ARIA_Q8A8 && dim != 256 && dim != 512 && dim != 768 && dim != 1024 && dim != 2048) {
+        /* the W8A8 norms quantise rows held in registers (k_rownorm's register path) */
+        aria_hip_set_error("aria_hip_dit_block_create: W8A8 needs dim 256, 512, 768, 1024 or 2048 (got %d)", dim);
+        return NULL;
+    }
     aria_hip_dit_block *b = (aria_hip_dit_block *)calloc(1, sizeof *b);
     if (!b) return NULL;
     b->dim = dim; b->H = num_heads; b->hd = head_dim; b->inner = inner; b->ffn = ffn; b->dim_ctx = dim_ctx;
     b->ffrows = ffn == ARIA_FFN_GLU ? 2 * inner : inner;
     b->prec = precision;
+    b->w8 = precision == ARIA_Q8A8;
     int attn_t, ffn_t;
     if (precision == ARIA_Q4) { attn_t = ARIA_WQ8; ffn_t = ARIA_WQ4; }
     else if (precision == ARIA_Q8 || precision == ARIA_Q8A8) { attn_t = ARIA_WQ8; ffn_t = ARIA_WQ8; }
@@ -186,6 +193,10 @@ size_t aria_hip_dit_block_weight_bytes(const aria_hip_dit_block *b) { return b ?
 typedef struct {
     uint16_t *h16, *q16, *k16, *v16, *att16, *ff16;
     float *big, *o;
+    /* W8A8 only: int8 activations [M, max(dim, inner)] + row scales [M], and the fp32
+     * producer output that is quantised (attention merge, FFN product) */
+    int8_t *xq;
+    float *sx, *f32;
 } wsl;
 
 #define WS_ALIGN 256
@@ -196,11 +207,16 @@ static size_t ws_layout(const aria_hip_dit_block *b, int B, int S, int Sc, char 
     /* big: the per-request cross K/V projection [B*Sc, 2*dim] fp32; the block's own
      * projections write through their fused epilogues (o is kept for layout only) */
     const size_t big = (size_t)B * Sc * 2 * d * 4;
-    const size_t sz[8] = {M * d * 2, big, M * d * 2, M * d * 2, M * d * 2, M * d * 2, 0,
-                          M * (size_t)b->inner * 2};
-    size_t off = 0, o[8];
-    for (int i = 0; i < 8; i++) { o[i] = off; off += al(sz[i]); }
+    const size_t wide = (size_t)(b->inner > b->dim ? b->inner : b->dim);
+    const size_t sz[11] = {M * d * 2, big, M * d * 2, M * d * 2, M * d * 2, M * d * 2, 0,
+                           M * (size_t)b->inner * 2,
+                           b->w8 ? M * wide : 0, b->w8 ? M * 4 : 0, b->w8 ? M * wide * 4 : 0};
+    size_t off = 0, o[11];
+    for (int i = 0; i < 11; i++) { o[i] = off; off += al(sz[i]); }
     if (base && w) {
+        w->xq = b->w8 ? (int8_t *)(base + o[8]) : NULL;
+        w->sx = b->w8 ? (float *)(base + o[9]) : NULL;
+        w->f32 = b->w8 ? (float *)(base + o[10]) : NULL;
         w->h16 = (uint16_t *)(base + o[0]);
         w->big = (float *)(base + o[1]);
         w->q16 = (uint16_t *)(base + o[2]);
@@ -291,6 +307,77 @@ int aria_hip_dit_block_forward_dev(aria_hip_dit_block *b, float *dx, int B, int 
                          aria_hip_stream(stream));
 }
 
+/* an int8 projection on the block's current int8 activations (w->xq, w->sx) */
+static hipError_t gemm_i8(const dmat *m, float *y, const wsl *w, const float *bias, int M, int gelu,
+                          const aria_qgemm_epi *e, hipStream_t s) {
+    return aria_k_gemm_i8(y, 0, w->xq, w->sx, (const int8_t *)m->q, m->scale, bias, M, m->K, m->N, gelu, e, s);
+}
+
+/* The W8A8 block (precision ARIA_Q8A8: the reference's h->w8a8 path, src/aria_cuda.cu:1055-1147,
+ * with aria_linear_q8a8's numbers): the same steps as block_forward with every projection on
+ * int8 activations. The reference keeps its producers in fp32 and quantises that output per
+ * row (gemm_w8a8); here the norms quantise their fp32 rows in registers and write int8 + row
+ * scales directly, and the attention outputs and the FFN product, whose rows span many
+ * workgroups, are written fp32 and quantised by aria_k_quant_act_q8. The int8 GEMMs carry the
+ * same fused epilogues (heads, gated residual, residual + local cond, GLU / GELU). */
+static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int B, int S, const float *const *tc,
+                            const float *const *gc, int gbs, const uint16_t *dk, const uint16_t *dv, int Sc,
+                            const float *dcos, const float *dsin, int rot, const float *dlocal, hipStream_t s) {
+    const int d = b->dim, H = b->H, M = B * S;
+    const float eps_norm = 1e-5f, eps_qk = 1e-6f;
+
+    /* ---- self-attention ---- */
+    STEP(aria_k_rownorm_ada_q8(w->xq, w->sx, dx, b->pre_norm, tc[0], tc[1], gc[0], gc[1], gbs, S, M, d, eps_norm, s),
+         "k_rownorm_q8 (pre_norm + adaLN)");
+    {
+        const int kind[3] = {0, 1, 2};
+        uint16_t *dst[3] = {w->q16, w->k16, w->v16};
+        const float *nw[3] = {b->sa_q_norm, b->sa_k_norm, NULL};
+        const aria_qgemm_epi e = epi_heads(S, H, 3, kind, dst, nw, dcos, dsin, rot, eps_qk);
+        STEP(gemm_i8(&b->sa_qkv, NULL, w, NULL, M, 0, &e, s), "k_gemm_i8 (sa_to_qkv + heads)");
+    }
+    STEP(aria_k_flash_attn(w->q16, w->k16, w->v16, w->f32, 0, B * H, H, S, S, s), "k_flash_attn (self)");
+    STEP(aria_k_quant_act_q8(w->xq, w->sx, w->f32, 0, M, d, s), "k_quant_act_q8 (self merge)");
+    {
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, tc[2], gc[2], gbs, NULL);
+        STEP(gemm_i8(&b->sa_out, dx, w, NULL, M, 0, &e, s), "k_gemm_i8 (sa_to_out + gated residual)");
+    }
+
+    /* ---- cross-attention ---- */
+    STEP(aria_k_rownorm_q8(w->xq, w->sx, dx, b->cross_norm, M, d, eps_norm, s), "k_rownorm_q8 (cross_norm)");
+    {
+        const int kind[1] = {0};
+        uint16_t *dst[1] = {w->q16};
+        const float *nw[1] = {b->ca_q_norm};
+        const aria_qgemm_epi e = epi_heads(S, H, 1, kind, dst, nw, NULL, NULL, 0, eps_qk);
+        STEP(gemm_i8(&b->ca_q, NULL, w, NULL, M, 0, &e, s), "k_gemm_i8 (ca_to_q + heads)");
+    }
+    STEP(aria_k_flash_attn(w->q16, dk, dv, w->f32, 0, B * H, H, S, Sc, s), "k_flash_attn (cross)");
+    STEP(aria_k_quant_act_q8(w->xq, w->sx, w->f32, 0, M, d, s), "k_quant_act_q8 (cross merge)");
+    {
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_ADD, S, NULL, NULL, 0, dlocal);
+        STEP(gemm_i8(&b->ca_out, dx, w, NULL, M, 0, &e, s), "k_gemm_i8 (ca_to_out + residual)");
+    }
+
+    /* ---- feed-forward ---- */
+    STEP(aria_k_rownorm_ada_q8(w->xq, w->sx, dx, b->ff_norm, tc[3], tc[4], gc[3], gc[4], gbs, S, M, d, eps_norm, s),
+         "k_rownorm_q8 (ff_norm + adaLN)");
+    if (b->ffn == ARIA_FFN_GLU) {
+        aria_qgemm_epi e;
+        memset(&e, 0, sizeof e);
+        e.mode = ARIA_EPI_GLU;
+        STEP(gemm_i8(&b->ff_in, w->f32, w, b->ff_in_b, M, 0, &e, s), "k_gemm_i8 (ff_in + GLU)");
+    } else {
+        STEP(gemm_i8(&b->ff_in, w->f32, w, b->ff_in_b, M, 1, NULL, s), "k_gemm_i8 (ff_in + GELU)");
+    }
+    STEP(aria_k_quant_act_q8(w->xq, w->sx, w->f32, 0, M, b->inner, s), "k_quant_act_q8 (ffn product)");
+    {
+        const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, tc[5], gc[5], gbs, NULL);
+        STEP(gemm_i8(&b->ff_out, dx, w, b->ff_out_b, M, 0, &e, s), "k_gemm_i8 (ff_out + gated residual)");
+    }
+    return 0;
+}
+
 /* dlocal: the inpaint local-additive conditioning [B*S, dim] added after the cross-attention
  * (src/aria_sa3_dit.c:248-252), or NULL */
 static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const float *dgcond, const uint16_t *dk,
@@ -318,6 +405,7 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
         gc[c] = dgcond ? dgcond + (size_t)c * d : NULL;
     }
     const int gbs = 6 * d;
+    if (b->w8) return block_forward_w8(b, &w, dx, B, S, tc, gc, gbs, dk, dv, Sc, dcos, dsin, rot, dlocal, s);
 
     /* ---- self-attention ---- */
     STEP(aria_k_rownorm_ada(w.h16, 1, dx, b->pre_norm, tc[0], tc[1], gc[0], gc[1], gbs, S, M, d, eps_norm, s),
@@ -444,7 +532,8 @@ aria_cuda_dit *aria_hip_dit_create_ex(const aria_sa3_dit_view *v, aria_dtype pre
         aria_hip_set_error("aria_cuda_dit_create: unsupported model shape");
         return NULL;
     }
-    if (precision == ARIA_DTYPE_AUTO) precision = ARIA_F32;   /* aria_cuda_int8_tc() == 0 here */
+    /* auto: W8A8 where the int8 matrix path exists, as the reference (src/aria_model_sa3.c:500-502) */
+    if (precision == ARIA_DTYPE_AUTO) precision = aria_cuda_int8_tc() ? ARIA_Q8A8 : ARIA_F32;
     aria_cuda_dit *h = (aria_cuda_dit *)calloc(1, sizeof *h);
     if (!h) return NULL;
     h->depth = v->depth; h->ed = v->ed; h->H = v->num_heads; h->inner = v->inner; h->io_ch = v->io_ch;

@@ -34,6 +34,14 @@ hipError_t aria_k_rownorm_ada(void *y, int out_f16, const float *x, const float 
                               const float *scale_t, const float *shift_t, const float *scale_g,
                               const float *shift_g, int g_bs, int rows_per_batch, int rows,
                               int dim, float eps, hipStream_t s);
+/* RMSNorm (w may be NULL) and RMSNorm + adaLN with W8A8 output: yq int8 [rows, dim] with
+ * sx[row] = amax / 127, the quantisation of the fp32 result (aria_k_quant_act_q8's rule);
+ * dim must be one the register path takes (256, 512, 768, 1024, 2048) */
+hipError_t aria_k_rownorm_q8(int8_t *yq, float *sx, const float *x, const float *w, int rows, int dim, float eps,
+                             hipStream_t s);
+hipError_t aria_k_rownorm_ada_q8(int8_t *yq, float *sx, const float *x, const float *w, const float *scale_t,
+                                 const float *shift_t, const float *scale_g, const float *shift_g, int g_bs,
+                                 int rows_per_batch, int rows, int dim, float eps, hipStream_t s);
 
 /* Elementwise (k_elementwise.hip). n counts floats. */
 hipError_t aria_k_add(float *y, const float *a, const float *b, size_t n, hipStream_t s);
@@ -101,7 +109,7 @@ enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2, ARIA_WI8 = 3 };
  *             kinds 0/1, copied for kind 2, and written fp16 to dst[sec] as
  *             [batch, heads, rows_per_batch, 64] (y unused)
  *   GLU       columns interleave (value, gate) pairs: y[m][c/2] = silu(gate) * value,
- *             fp16 [M, N/2] (the weight rows were interleaved when packed) */
+ *             [M, N/2], fp16 or fp32 (y_f16) (the weight rows were interleaved when packed) */
 enum { ARIA_EPI_STORE = 0, ARIA_EPI_GATE_RES = 1, ARIA_EPI_ADD = 2, ARIA_EPI_HEADS = 3, ARIA_EPI_GLU = 4 };
 typedef struct {
     int mode, rows_per_batch;

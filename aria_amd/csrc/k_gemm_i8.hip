@@ -34,19 +34,6 @@ __device__ __forceinline__ float4 qa_load(const void *x, size_t i) {
         return *reinterpret_cast<const float4 *>((const float *)x + i);
     }
 }
-/* rint (ties to even, as lrintf in the default rounding mode), clamp to [-127, 127], and
- * pack four int8 into one word */
-__device__ __forceinline__ uint32_t qa_pack(float4 v, float inv) {
-    const float f[4] = {v.x * inv, v.y * inv, v.z * inv, v.w * inv};
-    uint32_t w = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int q = min(max((int)__builtin_rintf(f[i]), -127), 127);
-        w |= (uint32_t)(q & 0xFF) << (8 * i);
-    }
-    return w;
-}
-
 template <bool F16>
 __global__ __launch_bounds__(256) void k_quant_act_q8(int8_t *xq, float *sx, const void *x, int M, int K) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -67,7 +54,7 @@ __global__ __launch_bounds__(256) void k_quant_act_q8(int8_t *xq, float *sx, con
         const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
 #pragma unroll
         for (int j = 0; j < QA_MAXV; j++)
-            if (j < nv) qr[lane + 64 * j] = qa_pack(v[j], inv);
+            if (j < nv) qr[lane + 64 * j] = q8_pack4(v[j], inv);
     } else if ((K & 3) == 0) {
         for (int k = 4 * lane; k < K; k += 256) {
             const float4 v = qa_load<F16>(x, base + k);
@@ -75,7 +62,7 @@ __global__ __launch_bounds__(256) void k_quant_act_q8(int8_t *xq, float *sx, con
         }
         mx = grp_max<64>(mx);
         const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
-        for (int k = 4 * lane; k < K; k += 256) qr[k >> 2] = qa_pack(qa_load<F16>(x, base + k), inv);
+        for (int k = 4 * lane; k < K; k += 256) qr[k >> 2] = q8_pack4(qa_load<F16>(x, base + k), inv);
     } else {   /* any K: one element per lane and step */
         auto ld1 = [&](int k) -> float {
             if constexpr (F16) return (float)__builtin_bit_cast(_Float16, ((const uint16_t *)x)[base + k]);

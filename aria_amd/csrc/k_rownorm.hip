@@ -32,7 +32,7 @@
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
 
-enum { EPI_MOD = 1, EPI_GELU = 2, EPI_RES = 4, EPI_F16 = 8, EPI_W = 16, EPI_B = 32, EPI_MADD = 64 };
+enum { EPI_MOD = 1, EPI_GELU = 2, EPI_RES = 4, EPI_F16 = 8, EPI_W = 16, EPI_B = 32, EPI_MADD = 64, EPI_Q8 = 128 };
 
 struct NormArgs {
     void *y;
@@ -45,6 +45,7 @@ struct NormArgs {
     int rows_per_batch, rows, dim;
     float eps;
     int gelu, resid, f16;
+    float *sx;   /* EPI_Q8: y is int8 [rows, dim] and sx[row] its scale (W8A8 activations) */
 };
 
 template <int NORM>
@@ -168,6 +169,27 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
         inv = (float)(1.0 / sqrt(s / dim + (double)a.eps));
     }
 
+    if constexpr ((EPI & EPI_Q8) != 0) {
+        /* W8A8: the fp32 row stays in registers, its absolute maximum is reduced across
+         * the row's lanes, and the row is written as int8 with sx = amax / 127 (the
+         * reference quantises the fp32 producer output the same way, src/aria_quant.c:258-270) */
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+            v[j].x = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].x, inv, mu, rstd, wv[j].x, bv[j].x), v[j].x, scv[j].x, shv[j].x);
+            v[j].y = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].y, inv, mu, rstd, wv[j].y, bv[j].y), v[j].y, scv[j].y, shv[j].y);
+            v[j].z = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].z, inv, mu, rstd, wv[j].z, bv[j].z), v[j].z, scv[j].z, shv[j].z);
+            v[j].w = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].w, inv, mu, rstd, wv[j].w, bv[j].w), v[j].w, scv[j].w, shv[j].w);
+            mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+        }
+        mx = grp_max<LPR>(mx);
+        const float qinv = mx > 0.0f ? 127.0f / mx : 0.0f;
+        uint32_t *yq = reinterpret_cast<uint32_t *>((int8_t *)a.y + (size_t)row * dim);
+#pragma unroll
+        for (int j = 0; j < VPL; j++) yq[j * LPR + l] = q8_pack4(v[j], qinv);
+        if (l == 0) a.sx[row] = mx / 127.0f;
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < VPL; j++) {
         const int c4 = j * LPR + l;
@@ -241,7 +263,9 @@ static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 /* the operand sets instantiated for the register path, per norm */
 using EpiRms = std::integer_sequence<int, 0, EPI_W, EPI_F16, EPI_F16 | EPI_W, EPI_MOD | EPI_W, EPI_MOD | EPI_F16 | EPI_W,
-                                      EPI_MOD | EPI_MADD | EPI_W, EPI_MOD | EPI_MADD | EPI_F16 | EPI_W>;
+                                      EPI_MOD | EPI_MADD | EPI_W, EPI_MOD | EPI_MADD | EPI_F16 | EPI_W,
+                                      EPI_Q8, EPI_Q8 | EPI_W, EPI_MOD | EPI_Q8 | EPI_W,
+                                      EPI_MOD | EPI_MADD | EPI_Q8 | EPI_W>;
 using EpiGemma = std::integer_sequence<int, 0, EPI_W>;
 using EpiLayer = std::integer_sequence<int, 0, EPI_W, EPI_B, EPI_W | EPI_B, EPI_MOD | EPI_GELU | EPI_RES,
                                         EPI_MOD | EPI_GELU | EPI_RES | EPI_W | EPI_B>;
@@ -273,7 +297,7 @@ static hipError_t launch_norm(const NormArgs &a, hipStream_t s) {
                      (!a.shift_add || al16(a.shift_add)) && a.mod_bs % 4 == 0 && a.add_bs % 4 == 0;
     const int epi = (a.scale ? EPI_MOD : 0) | (a.gelu ? EPI_GELU : 0) | (a.resid ? EPI_RES : 0) |
                     (a.f16 ? EPI_F16 : 0) | (a.w ? EPI_W : 0) | (a.b ? EPI_B : 0) |
-                    (a.scale && a.scale_add ? EPI_MADD : 0);
+                    (a.scale && a.scale_add ? EPI_MADD : 0) | (a.sx ? EPI_Q8 : 0);
     using Set = typename EpiSet<NORM>::type;
     bool hit = false;
     if (vec) {
@@ -288,7 +312,10 @@ static hipError_t launch_norm(const NormArgs &a, hipStream_t s) {
             default: break;
         }
     }
-    if (!hit) hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), dim3(256), 0, s, a);
+    if (!hit) {
+        if (a.sx) return hipErrorInvalidValue;   /* int8 output: register path only */
+        hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -302,7 +329,7 @@ extern "C" hipError_t aria_k_rownorm(void *y, int out_f16, const float *x, const
     a.scale_add = nullptr; a.shift_add = nullptr; a.mod_bs = dim; a.add_bs = 0;
     a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows;
     a.rows = rows; a.dim = dim; a.eps = eps;
-    a.gelu = gelu; a.resid = resid; a.f16 = out_f16;
+    a.gelu = gelu; a.resid = resid; a.f16 = out_f16; a.sx = nullptr;
     switch (norm) {
         case ARIA_NORM_GEMMA: return launch_norm<ARIA_NORM_GEMMA>(a, s);
         case ARIA_NORM_LAYER: return launch_norm<ARIA_NORM_LAYER>(a, s);
@@ -324,6 +351,34 @@ extern "C" hipError_t aria_k_rownorm_ada(void *y, int out_f16, const float *x, c
     a.scale_add = scale_g; a.shift_add = shift_g; a.mod_bs = 0; a.add_bs = g_bs;
     a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows;
     a.rows = rows; a.dim = dim; a.eps = eps;
-    a.gelu = 0; a.resid = 0; a.f16 = out_f16;
+    a.gelu = 0; a.resid = 0; a.f16 = out_f16; a.sx = nullptr;
+    return launch_norm<ARIA_NORM_RMS>(a, s);
+}
+
+/* The same two RMS forms with W8A8 output: yq int8 [rows, dim] and sx [rows], the
+ * quantisation of the fp32 result (dim 256..2048 in steps the register path takes). */
+extern "C" hipError_t aria_k_rownorm_q8(int8_t *yq, float *sx, const float *x, const float *w, int rows, int dim,
+                                        float eps, hipStream_t s) {
+    if (rows <= 0 || dim <= 0) return hipSuccess;
+    NormArgs a;
+    a.y = yq; a.x = x; a.w = w; a.b = nullptr; a.scale = nullptr; a.shift = nullptr;
+    a.scale_add = nullptr; a.shift_add = nullptr; a.mod_bs = dim; a.add_bs = 0;
+    a.rows_per_batch = rows; a.rows = rows; a.dim = dim; a.eps = eps;
+    a.gelu = 0; a.resid = 0; a.f16 = 0; a.sx = sx;
+    if (!sx || ((uintptr_t)yq & 3u)) return hipErrorInvalidValue;
+    return launch_norm<ARIA_NORM_RMS>(a, s);
+}
+extern "C" hipError_t aria_k_rownorm_ada_q8(int8_t *yq, float *sx, const float *x, const float *w,
+                                            const float *scale_t, const float *shift_t, const float *scale_g,
+                                            const float *shift_g, int g_bs, int rows_per_batch, int rows, int dim,
+                                            float eps, hipStream_t s) {
+    if (rows <= 0 || dim <= 0) return hipSuccess;
+    NormArgs a;
+    a.y = yq; a.x = x; a.w = w; a.b = nullptr; a.scale = scale_t; a.shift = shift_t;
+    a.scale_add = scale_g; a.shift_add = shift_g; a.mod_bs = 0; a.add_bs = g_bs;
+    a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows;
+    a.rows = rows; a.dim = dim; a.eps = eps;
+    a.gelu = 0; a.resid = 0; a.f16 = 0; a.sx = sx;
+    if (!sx || ((uintptr_t)yq & 3u)) return hipErrorInvalidValue;
     return launch_norm<ARIA_NORM_RMS>(a, s);
 }

@@ -227,13 +227,16 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
                     *reinterpret_cast<float4 *>((float *)a.y + (size_t)m * a.N + nb) =
                         make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
             }
-        } else if constexpr (MODE == ARIA_EPI_GLU) {   /* (value, gate) pairs -> silu(gate) * value, fp16 */
+        } else if constexpr (MODE == ARIA_EPI_GLU) {   /* (value, gate) pairs -> silu(gate) * value */
 #pragma unroll
             for (int it = 0; it < NIT; it++) {
                 const int m = mrow[it];
                 if (m >= a.M || !col_ok) continue;
-                *reinterpret_cast<uint32_t *>((uint16_t *)a.y + (size_t)m * (a.N >> 1) + (nb >> 1)) =
-                    pack2h(silu_f(v[it][1]) * v[it][0], silu_f(v[it][3]) * v[it][2]);
+                const float g0 = silu_f(v[it][1]) * v[it][0], g1 = silu_f(v[it][3]) * v[it][2];
+                if (a.y_f16)
+                    *reinterpret_cast<uint32_t *>((uint16_t *)a.y + (size_t)m * (a.N >> 1) + (nb >> 1)) = pack2h(g0, g1);
+                else   /* fp32 (the W8A8 block quantises the fp32 product) */
+                    *reinterpret_cast<float2 *>((float *)a.y + (size_t)m * (a.N >> 1) + (nb >> 1)) = make_float2(g0, g1);
             }
         } else if constexpr (MODE == ARIA_EPI_GATE_RES || MODE == ARIA_EPI_ADD) {
             /* read-modify-write of the fp32 residual: all loads first, then all stores */

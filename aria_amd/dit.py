@@ -34,7 +34,8 @@ class DitBlock:
     """One DiT block resident on the device.
 
     weights: dict of float32 numpy arrays keyed by BLOCK_FIELDS (missing local-cond
-    fields are fine). precision: Q4 (attention Q8 + FFN Q4), Q8, or F32/F16 (fp16).
+    fields are fine). precision: Q4 (attention Q8 + FFN Q4), Q8, Q8A8 (all Q8 with int8
+    activations, W8A8), or F32/F16 (fp16).
     """
 
     def __init__(self, weights, dim, num_heads, inner, dim_ctx, ffn=FFN_GLU, precision=Q4, head_dim=64):

@@ -25,7 +25,8 @@ extern "C" {
 int aria_cuda_available(void);
 /* src/aria_gpu.h:24 - 1 when the device beats the CPU path (CDNA3/CDNA4: gfx942, gfx950). */
 int aria_cuda_recommended(void);
-/* src/aria_gpu.h:25 - 1 when the W8A8 int8 path is served; 0 here (not built). */
+/* src/aria_gpu.h:25 - 1 when the W8A8 int8 path is served: on gfx950 (int8 MFMA), where
+ * aria_cuda_dit_create with ARIA_Q8A8 (and ARIA_DTYPE_AUTO) runs the int8 projections. */
 int aria_cuda_int8_tc(void);
 /* src/aria_gpu.h:27 - "name (gfxNNN, CUs, VRAM)" into buf. */
 void aria_cuda_device_info(char *buf, size_t buflen);

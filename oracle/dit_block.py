@@ -2,8 +2,9 @@
 
 Follows dit_block_core (src/aria_sa3_dit.c:141-312) step by step for one sequence
 (the reference is batch 1), with each projection dispatched like aria_linear_qw
-(src/aria_quant.c:419-430): Q8 -> aria_linear_q8, Q4 -> aria_linear_q4, F32 ->
-aria_linear. ``ops`` is the compiled reference (oracle.ref()) or the restatement
+(src/aria_quant.c:419-430): Q8 -> aria_linear_q8 (aria_linear_q8a8 with int8
+activations), Q4 -> aria_linear_q4, F32 -> aria_linear. ``ops`` is the compiled
+reference (oracle.ref()) or the restatement
 (oracle.port()); the block's static glue (adaln_modulate, gate_sigmoid, the GLU
 combine, extract/merge heads) comes from the restatement.
 
@@ -32,7 +33,8 @@ def merge(a):
 
 def pack_weights(ops, W, precision="q4"):
     """Per-projection packed form, the reference recipe (src/aria_sa3_dit.c:473-506):
-    q4 -> attention Q8 + FFN Q4; q8 -> all Q8; f32 -> fp32."""
+    q4 -> attention Q8 + FFN Q4; q8 -> all Q8; q8a8 -> all Q8 with int8 activations
+    (aria_qweight.a8, src/aria_quant.c:384, dispatched to aria_linear_q8a8); f32 -> fp32."""
     out = {}
     for name in ("sa_to_qkv", "sa_to_out", "ca_to_q", "ca_to_out", "ff_in_w", "ff_out_w"):
         ffn = name.startswith("ff_")
@@ -43,7 +45,7 @@ def pack_weights(ops, W, precision="q4"):
             out[name] = ("q4", q, s)
         else:
             q, s = ops.q8_quant(np.ascontiguousarray(W[name], np.float32))
-            out[name] = ("q8", q, s)
+            out[name] = ("q8a8" if precision == "q8a8" else "q8", q, s)
     return out
 
 
@@ -52,7 +54,7 @@ def dequantized(P, W, packed):
     reference's fp32 block forward computes what the dequant-on-use path computes."""
     Wd = dict(W)
     for name, pk in packed.items():
-        if pk[0] == "q8":
+        if pk[0] in ("q8", "q8a8"):
             Wd[name] = P.q8_dequant(pk[1], pk[2])
         elif pk[0] == "q4":
             Wd[name] = P.q4_dequant(pk[1], pk[2], W[name].shape[1])
@@ -80,6 +82,8 @@ def block_forward(ops, P, x, kc, vc, gcond, W, packed, cos_t, sin_t, rot, H, ffn
         h = np.ascontiguousarray(h, np.float32)
         if pk[0] == "q8":
             return ops.linear_q8(h, pk[1], pk[2], bias)
+        if pk[0] == "q8a8":
+            return ops.linear_q8a8(h, pk[1], pk[2], bias)
         if pk[0] == "q4":
             return ops.linear_q4(h, pk[1], pk[2], bias)
         return ops.linear(h, pk[1], bias)

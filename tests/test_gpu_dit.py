@@ -20,7 +20,7 @@ from conftest import assert_close, randn, rng
 pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 2e-3, 5e-3
-PNAME = {4: "q4", 3: "q8", 0: "f32"}
+PNAME = {4: "q4", 3: "q8", 0: "f32", 5: "q8a8"}
 
 
 @pytest.fixture
@@ -59,11 +59,12 @@ def ref_step(R, port, M, precision, x_CT, ced, gcond, c, s, rot, H, local=None, 
             kc, vc = DB.cross_kv(R, ced, W, H)
             seq = DB.block_forward(R, port, seq, kc, vc, gcond, Wd, DB.pack_weights(R, Wd, "f32"), c, s, rot, H,
                                    DB.FFN_GELU)
-        elif local is None:
+        elif local is None and PNAME[precision] != "q8a8":
             seq = R.dit_block_forward(seq, ced, gcond, c, s, rot, DB.dequantized(port, W, packed), H, inner)
         else:
             kc, vc = DB.cross_kv(R, ced, W, H)
-            seq = DB.block_forward(R, port, seq, kc, vc, gcond, W, packed, c, s, rot, H, DB.FFN_GLU, local[b])
+            seq = DB.block_forward(R, port, seq, kc, vc, gcond, W, packed, c, s, rot, H, DB.FFN_GLU,
+                                   None if local is None else local[b])
     out = R.linear(np.ascontiguousarray(seq[n_mem:]), M["project_out"])
     out = out + R.linear(out, M["postprocess"])
     return np.ascontiguousarray(out.T)
@@ -90,6 +91,25 @@ def test_dit_step_parity(hip, port, R, precision):
         got = dit.step(x, g)
         want = ref_step(R, port, M, precision, x[0], ced[0], g[0], c, s, rot, H)
         assert_close(got[0], want, ATOL, RTOL, f"dit step {k} {PNAME[precision]}")
+    dit.free()
+
+
+def test_dit_step_parity_w8a8(hip, port, R):
+    """aria_cuda_dit_step with ARIA_Q8A8 (int8 activations on every Q8 projection; the W8A8
+    norms need ed >= 256): against the composition of reference ops with aria_linear_q8a8."""
+    M = model(17, ed=256, inner=512)
+    T, n_cond, H, rot = 40, 12, 4, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = R.rope_freqs(S, rot, 10000.0)
+    dit = make_dit(M, 5, H, rot)
+    _, ced, _ = inputs(3, 1, io_ch, T, n_cond, ed)
+    dit.set_request(T, [ced[0]], c, s)
+    for k in range(2):
+        x, _, g = inputs(200 + k, 1, io_ch, T, n_cond, ed)
+        got = dit.step(x, g)
+        want = ref_step(R, port, M, 5, x[0], ced[0], g[0], c, s, rot, H)
+        assert_close(got[0], want, ATOL, RTOL, f"dit step {k} q8a8")
     dit.free()
 
 
