@@ -33,6 +33,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, AMD published
 FP16_PEAK_TFLOPS = 2500.0      # MI355X dense fp16 MFMA, AMD published
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, AMD published
 B, S, D, H, HD = 2, 1296, 1024, 16, 64
 SEED = 0xA21A0000
 
@@ -330,7 +331,9 @@ def main():
 
 def gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps):
     """Config 3: X [2592,K] ~N(0,1) times W [N,K] ~N(0,0.02) packed on the device (bit-exact with
-    the reference quantizer), for (K,N) = (1024,4096) and (4096,1024), Q8 and Q4."""
+    the reference quantizer), for (K,N) = (1024,4096) and (4096,1024), Q8 and Q4; w8a8 is the same
+    Q8 weight with the reference's W8A8 numbers (aria_linear_q8a8: per-row int8 quantisation of
+    the fp32 X, then the int8 MFMA GEMM; both launches timed, int8 ops counted as 2 M N K)."""
     out = {}
     M = B * S
     for K, N in ((1024, 4096), (4096, 1024)):
@@ -353,6 +356,15 @@ def gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps):
             key = f"{'q8' if wt == 0 else 'q4'}_M{M}_K{K}_N{N}"
             out[key] = {"us": round(ms * 1e3, 2), "us_min": round(ms_min * 1e3, 2), "TFLOP/s": round(tf, 1),
                         "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 3), "flop": flop}
+        wsb = int(L.aria_hip_q8a8_ws_bytes(M, K))
+        dws = DeviceArray((wsb,), np.uint8)
+        fn = (lambda i: L.aria_hip_linear_q8a8_dev(dy.p, dx[i % 2].p, 0, dq8.p, ds8.p, None, M, K, N, dws.p, stream))
+        for i in range(3):
+            chk(fn(i))
+        ms, ms_min = time_loop(fn, reps)
+        tf = flop / (ms * 1e-3) / 1e12
+        out[f"w8a8_M{M}_K{K}_N{N}"] = {"us": round(ms * 1e3, 2), "us_min": round(ms_min * 1e3, 2), "TOP/s": round(tf, 1),
+                                       "frac_int8_peak": round(tf / INT8_PEAK_TOPS, 3), "ops": flop}
     return out
 
 
@@ -360,8 +372,10 @@ def block_leg(DeviceArray, time_loop, stream, rng, reps):
     """Config 4: one random-init q4 DiT block (attention projections Q8, FFN Q4, ca_to_kv fp16),
     x [2,1296,1024] ~N(0,1), cond [2,256,768] ~N(0,1), weights ~N(0,0.02), gains 1+N(0,0.02),
     modulation [2, 6*1024] ~N(0,0.1), 16 heads x 64, RoPE rot 32. Timed: the block forward
-    (the per-request cross K/V projection runs once, outside)."""
-    from aria_amd.dit import DitBlock, random_block_weights, FFN_GELU, FFN_GLU, Q4
+    (the per-request cross K/V projection runs once, outside). The *_w8a8 entries are the same
+    block in the reference's W8A8 mode (ARIA_Q8A8: every projection Q8 with per-row int8
+    activations on the int8 MFMA)."""
+    from aria_amd.dit import DitBlock, random_block_weights, FFN_GELU, FFN_GLU, Q4, Q8A8
     Bb, Sb, Sc, dim, H, inner, dctx = B, S, 256, 1024, 16, 4096, 768
     M = Bb * Sb
     out = {}
@@ -369,9 +383,10 @@ def block_leg(DeviceArray, time_loop, stream, rng, reps):
     ang = np.arange(Sb)[:, None] * inv[None, :]
     dcos = DeviceArray.from_host(np.cos(ang).astype(np.float32))
     dsin = DeviceArray.from_host(np.sin(ang).astype(np.float32))
-    for name, ffn in (("gelu", FFN_GELU), ("glu", FFN_GLU)):
+    for name, ffn, prec in (("gelu", FFN_GELU, Q4), ("glu", FFN_GLU, Q4), ("gelu_w8a8", FFN_GELU, Q8A8),
+                            ("glu_w8a8", FFN_GLU, Q8A8)):
         W = random_block_weights(rng, dim, inner, dctx, ffn=ffn)
-        blk = DitBlock(W, dim, H, inner, dctx, ffn=ffn, precision=Q4)
+        blk = DitBlock(W, dim, H, inner, dctx, ffn=ffn, precision=prec)
         dctxa = DeviceArray.from_host(rng.standard_normal((Bb * Sc, dctx), dtype=np.float32))
         dk, dv = blk.cross_kv(dctxa, Bb, Sc, stream)
         dx = DeviceArray.from_host(rng.standard_normal((M, dim), dtype=np.float32))
