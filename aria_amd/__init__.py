@@ -91,6 +91,7 @@ SIGNATURES = {
     "aria_hip_q8_dequant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
     "aria_hip_q4_dequant_dev": (_i, [_P, _P, _P, _i, _i, _P]),
     "aria_hip_qlinear_dev": (_i, [_P, _i, _P, _i, _i, _P, _P, _P, _i, _i, _i, _P]),
+    "aria_hip_rmsnorm_adaln_q8_dev": (_i, [_P, _P, _P, _P, _P, _P, _i, _i, _i, _f, _P]),
     "aria_hip_quant_act_q8_dev": (_i, [_P, _P, _P, _i, _i, _i, _P]),
     "aria_hip_gemm_i8_dev": (_i, [_P, _i, _P, _P, _P, _P, _P, _i, _i, _i, _P]),
     "aria_hip_q8a8_ws_bytes": (_sz, [_i, _i]),

@@ -510,7 +510,18 @@ int aria_hip_linear_q4_dev(float *dy, const float *dx, const uint8_t *dq, const 
     return aria_hip_qlinear_dev(dy, 0, dx, 0, ARIA_WQ4, dq, dscale, db, M, K, N, stream);
 }
 
-/* W8A8 (k_gemm_i8.hip) */
+/* W8A8 (k_gemm_i8.hip, the int8-output norms of k_rownorm.hip) */
+int aria_hip_rmsnorm_adaln_q8_dev(int8_t *dyq, float *dsx, const float *dx, const float *dw, const float *dsc,
+                                  const float *dsh, int rows, int dim, int rpb, float eps, void *stream) {
+    ENSURE();
+    REQ(rows >= 0 && (dim == 256 || dim == 512 || dim == 768 || dim == 1024 || dim == 2048));
+    REQ(rows == 0 || (dyq && dsx && dx && !dsc == !dsh));
+    REQ(rpb >= 0 && (rpb == 0 || rows % rpb == 0));
+    REQ((((uintptr_t)dyq & 3u) | ((uintptr_t)dx & 15u) | ((uintptr_t)dw & 15u) | ((uintptr_t)dsc & 15u) |
+         ((uintptr_t)dsh & 15u)) == 0);
+    KCK(aria_k_rownorm_q8(dyq, dsx, dx, dw, dsc, dsh, rpb, rows, dim, eps, pick(stream)), "k_rownorm_q8");
+    return 0;
+}
 int aria_hip_quant_act_q8_dev(int8_t *dxq, float *dsx, const void *dx, int x_f16, int M, int K, void *stream) {
     ENSURE();
     REQ(M >= 0 && K > 0 && (M == 0 || (dxq && dsx && dx)));

@@ -344,7 +344,8 @@ static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int 
     }
 
     /* ---- cross-attention ---- */
-    STEP(aria_k_rownorm_q8(w->xq, w->sx, dx, b->cross_norm, M, d, eps_norm, s), "k_rownorm_q8 (cross_norm)");
+    STEP(aria_k_rownorm_q8(w->xq, w->sx, dx, b->cross_norm, NULL, NULL, 0, M, d, eps_norm, s),
+         "k_rownorm_q8 (cross_norm)");
     {
         const int kind[1] = {0};
         uint16_t *dst[1] = {w->q16};

@@ -34,11 +34,12 @@ hipError_t aria_k_rownorm_ada(void *y, int out_f16, const float *x, const float 
                               const float *scale_t, const float *shift_t, const float *scale_g,
                               const float *shift_g, int g_bs, int rows_per_batch, int rows,
                               int dim, float eps, hipStream_t s);
-/* RMSNorm (w may be NULL) and RMSNorm + adaLN with W8A8 output: yq int8 [rows, dim] with
- * sx[row] = amax / 127, the quantisation of the fp32 result (aria_k_quant_act_q8's rule);
+/* RMSNorm (w may be NULL; scale / shift per batch [rows / rows_per_batch, dim] or NULL) and
+ * RMSNorm + adaLN with the modulation formed in place, with W8A8 output: yq int8 [rows, dim]
+ * with sx[row] = amax / 127, the quantisation of the fp32 result (aria_k_quant_act_q8's rule);
  * dim must be one the register path takes (256, 512, 768, 1024, 2048) */
-hipError_t aria_k_rownorm_q8(int8_t *yq, float *sx, const float *x, const float *w, int rows, int dim, float eps,
-                             hipStream_t s);
+hipError_t aria_k_rownorm_q8(int8_t *yq, float *sx, const float *x, const float *w, const float *scale,
+                             const float *shift, int rows_per_batch, int rows, int dim, float eps, hipStream_t s);
 hipError_t aria_k_rownorm_ada_q8(int8_t *yq, float *sx, const float *x, const float *w, const float *scale_t,
                                  const float *shift_t, const float *scale_g, const float *shift_g, int g_bs,
                                  int rows_per_batch, int rows, int dim, float eps, hipStream_t s);

@@ -264,7 +264,7 @@ static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 /* the operand sets instantiated for the register path, per norm */
 using EpiRms = std::integer_sequence<int, 0, EPI_W, EPI_F16, EPI_F16 | EPI_W, EPI_MOD | EPI_W, EPI_MOD | EPI_F16 | EPI_W,
                                       EPI_MOD | EPI_MADD | EPI_W, EPI_MOD | EPI_MADD | EPI_F16 | EPI_W,
-                                      EPI_Q8, EPI_Q8 | EPI_W, EPI_MOD | EPI_Q8 | EPI_W,
+                                      EPI_Q8, EPI_Q8 | EPI_W, EPI_MOD | EPI_Q8, EPI_MOD | EPI_Q8 | EPI_W,
                                       EPI_MOD | EPI_MADD | EPI_Q8 | EPI_W>;
 using EpiGemma = std::integer_sequence<int, 0, EPI_W>;
 using EpiLayer = std::integer_sequence<int, 0, EPI_W, EPI_B, EPI_W | EPI_B, EPI_MOD | EPI_GELU | EPI_RES,
@@ -355,15 +355,17 @@ extern "C" hipError_t aria_k_rownorm_ada(void *y, int out_f16, const float *x, c
     return launch_norm<ARIA_NORM_RMS>(a, s);
 }
 
-/* The same two RMS forms with W8A8 output: yq int8 [rows, dim] and sx [rows], the
- * quantisation of the fp32 result (dim 256..2048 in steps the register path takes). */
-extern "C" hipError_t aria_k_rownorm_q8(int8_t *yq, float *sx, const float *x, const float *w, int rows, int dim,
-                                        float eps, hipStream_t s) {
+/* The two RMS forms with W8A8 output: yq int8 [rows, dim] and sx [rows], the quantisation
+ * of the fp32 result (dim 256..2048 in steps the register path takes). aria_k_rownorm_q8
+ * takes scale / shift per batch ([rows / rows_per_batch, dim], both NULL for a plain norm). */
+extern "C" hipError_t aria_k_rownorm_q8(int8_t *yq, float *sx, const float *x, const float *w, const float *scale,
+                                        const float *shift, int rows_per_batch, int rows, int dim, float eps,
+                                        hipStream_t s) {
     if (rows <= 0 || dim <= 0) return hipSuccess;
     NormArgs a;
-    a.y = yq; a.x = x; a.w = w; a.b = nullptr; a.scale = nullptr; a.shift = nullptr;
+    a.y = yq; a.x = x; a.w = w; a.b = nullptr; a.scale = scale; a.shift = shift;
     a.scale_add = nullptr; a.shift_add = nullptr; a.mod_bs = dim; a.add_bs = 0;
-    a.rows_per_batch = rows; a.rows = rows; a.dim = dim; a.eps = eps;
+    a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows; a.rows = rows; a.dim = dim; a.eps = eps;
     a.gelu = 0; a.resid = 0; a.f16 = 0; a.sx = sx;
     if (!sx || ((uintptr_t)yq & 3u)) return hipErrorInvalidValue;
     return launch_norm<ARIA_NORM_RMS>(a, s);

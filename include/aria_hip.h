@@ -154,6 +154,15 @@ int aria_hip_linear_q4_dev(float *dy, const float *dx, const uint8_t *dq, const 
  * activation quantisation k_quant_act_q8(_h), int8 IMMA GEMM into int32, dequant k_deq_i32)
  * with the numbers of aria_linear_q8a8 (src/aria_quant.h:47-51, src/aria_quant.c:253-345),
  * bit for bit. */
+/* RMSNorm(w) (-> adaLN modulate with per-batch dscale / dshift [rows / rows_per_batch, dim],
+ * or both NULL) with W8A8 output, one pass: the fp32 result row (the aria_hip_rmsnorm_adaln_dev
+ * value) is quantised in registers as aria_hip_quant_act_q8_dev does, dyq int8 [rows, dim] and
+ * dsx [rows]. The reference's W8A8 block runs k_rmsnorm(_adaln) into fp32 then
+ * k_quant_act_q8 (src/aria_cuda.cu:1075, 1094, 1133 with 934-949). dim 256, 512, 768, 1024 or
+ * 2048. */
+int aria_hip_rmsnorm_adaln_q8_dev(int8_t *dyq, float *dsx, const float *dx, const float *dw, const float *dscale,
+                                  const float *dshift, int rows, int dim, int rows_per_batch, float eps,
+                                  void *stream);
 /* Per-row symmetric int8 activations: sx[m] = amax / 127 (amax = max |x[m,:]|),
  * dxq[m,k] = clamp(rint(x * 127 / amax), -127, 127), all zero when amax == 0. dx is
  * fp32 or fp16 (x_f16) [M, K]; dxq [M, K] int8, dsx [M]. */

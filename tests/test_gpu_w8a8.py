@@ -103,3 +103,33 @@ def test_w8a8_device_api(hip, port):
     # empty shapes are no-ops
     hip.check(L.aria_hip_linear_q8a8_dev(dy.p, dx.p, 0, dq.p, ds.p, None, 0, K, N, dws.p, None))
     hip.check(L.aria_hip_gemm_i8_dev(dy.p, 0, dxq.p, dsx.p, dq.p, ds.p, None, M, K, 0, None))
+
+
+def test_rmsnorm_q8_fused(hip, port):
+    """The W8A8 producers: RMSNorm(w) (-> adaLN, per-batch modulation) quantised in registers,
+    against the oracle's fp32 norm composition then or_quant_act_q8. The fp32 norm matches the
+    oracle to the last bit on nearly every element (test_gpu_ops), so the int8 rows and scales
+    agree except where a 1-ulp difference crosses a rounding boundary or moves the row max."""
+    from aria_amd.device import DeviceArray, sync
+    L = hip.lib()
+    r = rng(41)
+    B, S, D = 2, 75, 1024
+    x = randn(r, (B * S, D)); w = (1 + randn(r, D, 0.02)).astype(np.float32)
+    sc = randn(r, (B, D), 0.1); sh = randn(r, (B, D), 0.1)
+    x[3] = 0.0                                             # zero row: sx 0, xq 0
+    dx, dw, dsc, dsh = (DeviceArray.from_host(a) for a in (x, w, sc, sh))
+    dq = DeviceArray((B * S, D), np.int8)
+    ds = DeviceArray((B * S,), np.float32)
+    for mod in (True, False):
+        hip.check(L.aria_hip_rmsnorm_adaln_q8_dev(dq.p, ds.p, dx.p, dw.p, dsc.p if mod else None,
+                                                  dsh.p if mod else None, B * S, D, S, 1e-5, None))
+        sync()
+        y = np.concatenate([port.adaln_modulate(port.rmsnorm(x[b * S:(b + 1) * S], w, 1e-5), sc[b], sh[b])
+                            if mod else port.rmsnorm(x[b * S:(b + 1) * S], w, 1e-5) for b in range(B)])
+        xq, sx = port.quant_act_q8(np.ascontiguousarray(y, np.float32))
+        gq, gs = dq.to_host(), ds.to_host()
+        assert np.mean(gq == xq) > 0.9999 and np.abs(gq.astype(np.int32) - xq).max() <= 1, mod
+        assert np.mean(bits(gs) == bits(sx)) > 0.97 and np.allclose(gs, sx, rtol=1e-6, atol=0), mod
+        if not mod:                                        # (with adaLN the zero row becomes shift)
+            assert gs[3] == 0.0 and np.all(gq[3] == 0)
+    assert L.aria_hip_rmsnorm_adaln_q8_dev(dq.p, ds.p, dx.p, dw.p, None, None, B * S, 100, 0, 1e-5, None) == -1
