@@ -90,14 +90,25 @@ __global__ __launch_bounds__(256) void k_quant_act_q8(int8_t *xq, float *sx, con
 /* activation tile [BM][64] bytes: chunk c (16 B) of row r at c ^ ((r >> 2) & 3), so 16
  * lanes reading one chunk of 16 consecutive rows touch all 64 banks once */
 __device__ __forceinline__ int ioff(int r, int c) { return r * IBK + ((c ^ ((r >> 2) & 3)) << 4); }
+/* 128-byte rows (K-tile 128): chunk c of row r at c ^ ((r >> 1) & 7), the same property */
+template <int KB>
+__device__ __forceinline__ int ioffk(int r, int c) {
+    if constexpr (KB == 64) return ioff(r, c);
+    else return r * KB + ((c ^ ((r >> 1) & 7)) << 4);
+}
 
-template <int FM, int MINB, int MODE, bool GELU>
+/* KB: K-tile depth in bytes (64, or 128 with K % 128 == 0): lane half h covers k in
+ * [KB/2 h, KB/2 (h + 1)) of the tile, MFMA step ks (KB / 32 of them) its 16 k at KB/2 h + 16 ks */
+template <int FM, int MINB, int MODE, bool GELU, int KB = 64>
 __global__ __launch_bounds__(256, MINB) void k_gemm_i8(QArgs a, int NTN, int T) {
+    static_assert(KB == 64 || KB == 128, "K-tile");
+    constexpr int NKS = KB / 32;              /* MFMA steps per K-tile */
     constexpr int FN = 2, BM = 32 * FM, BN = 256;
     constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
-    constexpr int TILE_BYTES = 2 * BM * IBK, EPI_BYTES = 4 * 32 * EPI_STRIDE;
+    constexpr int TILE_BYTES = 2 * BM * KB, EPI_BYTES = 4 * 32 * EPI_STRIDE;
     constexpr int LDS_BYTES = TILE_BYTES > EPI_BYTES ? TILE_BYTES : EPI_BYTES;
-    constexpr int XC = BM * 4;                /* 16-byte chunks of one activation tile */
+    constexpr int CPR = KB / 16;              /* 16-byte chunks per row */
+    constexpr int XC = BM * CPR;              /* 16-byte chunks of one activation tile */
     constexpr int XPT = (XC + 255) / 256;     /* chunks per thread */
     __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
@@ -106,19 +117,22 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_i8(QArgs a, int NTN, int T) 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lrow = lane & 31, lh = lane >> 5;
     const int m0 = (t / NTN) * BM, n0 = (t % NTN) * BN;
-    const int KT = a.K / IBK;
+    const int KT = a.K / KB;
     const int8_t *xq = (const int8_t *)a.x, *wq = (const int8_t *)a.q;
 
     /* weight rows of this lane (rows past N re-read the last row; never stored) */
-    const int8_t *wrow0 = wq + (size_t)min(n0 + wave * 64 + lrow, a.N - 1) * a.K + 32 * lh;
-    const int8_t *wrow1 = wq + (size_t)min(n0 + wave * 64 + 32 + lrow, a.N - 1) * a.K + 32 * lh;
-    typedef uint32_t ws_t __attribute__((ext_vector_type(16)));   /* [block 0: 8 words, block 1: 8 words] */
+    const int8_t *wrow0 = wq + (size_t)min(n0 + wave * 64 + lrow, a.N - 1) * a.K + (KB / 2) * lh;
+    const int8_t *wrow1 = wq + (size_t)min(n0 + wave * 64 + 32 + lrow, a.N - 1) * a.K + (KB / 2) * lh;
+    /* [block 0: 4 NKS words, block 1: 4 NKS words] */
+    typedef uint32_t ws_t __attribute__((ext_vector_type(8 * NKS)));
     auto wload = [&](ws_t &s, int kt) __attribute__((always_inline)) {
-        const uint4 *p0 = reinterpret_cast<const uint4 *>(wrow0 + kt * IBK);
-        const uint4 *p1 = reinterpret_cast<const uint4 *>(wrow1 + kt * IBK);
-        const uint4 u[4] = {p0[0], p0[1], p1[0], p1[1]};
+        const uint4 *p0 = reinterpret_cast<const uint4 *>(wrow0 + kt * KB);
+        const uint4 *p1 = reinterpret_cast<const uint4 *>(wrow1 + kt * KB);
+        uint4 u[2 * NKS];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < NKS; i++) { u[i] = p0[i]; u[NKS + i] = p1[i]; }
+#pragma unroll
+        for (int i = 0; i < 2 * NKS; i++) {
             s[4 * i] = u[i].x; s[4 * i + 1] = u[i].y; s[4 * i + 2] = u[i].z; s[4 * i + 3] = u[i].w;
         }
     };
@@ -129,18 +143,19 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_i8(QArgs a, int NTN, int T) 
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
             const int c = (XC % 256 == 0) ? tid + 256 * i : min(tid + 256 * i, XC - 1);
-            const int m = min(m0 + (c >> 2), a.M - 1);
-            const uint4 u = *reinterpret_cast<const uint4 *>(xq + (size_t)m * a.K + kt * IBK + 16 * (c & 3));
+            const int m = min(m0 + c / CPR, a.M - 1);
+            const uint4 u = *reinterpret_cast<const uint4 *>(xq + (size_t)m * a.K + kt * KB + 16 * (c % CPR));
             r[4 * i] = u.x; r[4 * i + 1] = u.y; r[4 * i + 2] = u.z; r[4 * i + 3] = u.w;
         }
     };
     auto xstore = [&](const xs_t &r, int buf) __attribute__((always_inline)) {
-        uint8_t *X = lds + buf * (BM * IBK);
+        uint8_t *X = lds + buf * (BM * KB);
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
             const int c = tid + 256 * i;
             if (XC % 256 == 0 || c < XC)
-                *reinterpret_cast<uint4 *>(X + ioff(c >> 2, c & 3)) = make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
+                *reinterpret_cast<uint4 *>(X + ioffk<KB>(c / CPR, c % CPR)) =
+                    make_uint4(r[4 * i], r[4 * i + 1], r[4 * i + 2], r[4 * i + 3]);
         }
     };
 
@@ -153,17 +168,19 @@ __global__ __launch_bounds__(256, MINB) void k_gemm_i8(QArgs a, int NTN, int T) 
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
     auto compute = [&](ws_t &ws, int buf) __attribute__((always_inline)) {
-        const uint8_t *X = lds + buf * (BM * IBK);
-        i32x4_t xf[2][FM];
+        const uint8_t *X = lds + buf * (BM * KB);
+        i32x4_t xf[NKS][FM];
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++)
+        for (int ks = 0; ks < NKS; ks++)
 #pragma unroll
             for (int i = 0; i < FM; i++)
-                xf[ks][i] = *reinterpret_cast<const i32x4_t *>(X + ioff(i * 32 + lrow, 2 * lh + ks));
+                xf[ks][i] = *reinterpret_cast<const i32x4_t *>(X + ioffk<KB>(i * 32 + lrow, NKS * lh + ks));
 #pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
+        for (int ks = 0; ks < NKS; ks++) {
+            constexpr int B1 = 4 * NKS;   /* block 1's first word */
             const i32x4_t w0 = {(int)ws[4 * ks], (int)ws[4 * ks + 1], (int)ws[4 * ks + 2], (int)ws[4 * ks + 3]};
-            const i32x4_t w1 = {(int)ws[8 + 4 * ks], (int)ws[9 + 4 * ks], (int)ws[10 + 4 * ks], (int)ws[11 + 4 * ks]};
+            const i32x4_t w1 = {(int)ws[B1 + 4 * ks], (int)ws[B1 + 4 * ks + 1], (int)ws[B1 + 4 * ks + 2],
+                                (int)ws[B1 + 4 * ks + 3]};
 #pragma unroll
             for (int i = 0; i < FM; i++) {
                 acc[i][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w0, xf[ks][i], acc[i][0], 0, 0, 0);
@@ -238,6 +255,12 @@ static void launch_i8_m(const QArgs &a, hipStream_t s) {
     constexpr int BM = 32 * FM, BN = 256;
     const int MT = (a.M + BM - 1) / BM, NTN = (a.N + BN - 1) / BN, T = MT * NTN;
     const int grid = ((T + 7) / 8) * 8;
+    if constexpr (FM == 2) {
+        if (a.K % 128 == 0) {   /* fewer barriers per MFMA where the tiles are short */
+            hipLaunchKernelGGL((k_gemm_i8<FM, 2, MODE, GELU, 128>), dim3(grid), dim3(256), 0, s, a, NTN, T);
+            return;
+        }
+    }
     hipLaunchKernelGGL((k_gemm_i8<FM, (FM <= 2 ? 2 : 1), MODE, GELU>), dim3(grid), dim3(256), 0, s, a, NTN, T);
 }
 template <int FM>
