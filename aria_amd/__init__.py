@@ -121,6 +121,7 @@ SIGNATURES = {
     "aria_hip_dit_device_buffers": (_i, [_P, _P, _P, _P]),
     "aria_hip_dit_run": (_i, [_P, _P]),
     "aria_hip_dit_graph_active": (_i, [_P]),
+    "aria_hip_dit_load_overlay": (_i, [_P, C.c_char_p]),
     "aria_cuda_dec_create": (_P, [_P]),
     "aria_cuda_dec_free": (None, [_P]),
     "aria_cuda_dec_forward": (None, [_P, _P, _P, _i]),

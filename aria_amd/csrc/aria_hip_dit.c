@@ -27,6 +27,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include "aria_dit.h"
+#include "aria_gpu.h"
 #include "aria_hip.h"
 #include "aria_hip_internal.h"
 #include "aria_hip_kernels.h"
@@ -766,6 +767,103 @@ static int dit_run(aria_cuda_dit *h, hipStream_t s) {
 }
 
 int aria_hip_dit_graph_active(const aria_cuda_dit *h) { return h && h->graph_ready; }
+
+/* ---- the reference's packed DiT overlay (.aria) ----
+ * File (aria_sa3_dit_quant_save, src/aria_sa3_dit.c:509-527): "ARIAQNT1", int32 {dt, depth, ed,
+ * inner}, then per block six records in the order sa_to_qkv, sa_to_out, ca_to_q, ca_to_out,
+ * ff_in_w, ff_out_w (src/aria_sa3_dit.c:512-516), each as aria_qweight_write lays it out
+ * (src/aria_quant.c:439-449): int32 {dt, N, K}, u64 qbytes, the packed bytes, u64 nscale, the
+ * fp32 scales. The records replace the blocks' projections as they are: no quantisation, on
+ * the host or the device. */
+static int ov_read(FILE *f, void *p, size_t n) { return fread(p, 1, n, f) == n ? 0 : -1; }
+
+static int ov_record(FILE *f, int N, int K, int glu_rows, int want_q8, dmat *out, size_t *acc) {
+    int32_t hdr[3];
+    uint64_t qb64 = 0, ns64 = 0;
+    if (ov_read(f, hdr, sizeof hdr)) return -1;
+    const int dt = hdr[0];
+    if ((dt != ARIA_Q8 && dt != ARIA_Q4) || hdr[1] != N || hdr[2] != K || (want_q8 && dt != ARIA_Q8)) return -2;
+    const size_t rb = dt == ARIA_Q8 ? (size_t)K : (size_t)(K + 1) / 2;        /* bytes per row */
+    const size_t sr = dt == ARIA_Q8 ? 1 : (size_t)2 * ((K + 31) / 32);       /* scales per row */
+    if (ov_read(f, &qb64, 8) || qb64 != rb * N) return -2;
+    uint8_t *q = (uint8_t *)malloc(rb * N), *qi = NULL;
+    float *sc = NULL, *si = NULL;
+    int rc = q ? ov_read(f, q, rb * N) : -3;
+    if (!rc && (ov_read(f, &ns64, 8) || ns64 != sr * N)) rc = -2;
+    if (!rc) rc = (sc = (float *)malloc(sr * N * sizeof(float))) ? ov_read(f, sc, sr * N * sizeof(float)) : -3;
+    if (!rc && glu_rows) {   /* GLU: rows (value_i, gate_i) interleaved, as block create packs them */
+        const int inner = N / 2;
+        qi = (uint8_t *)malloc(rb * N);
+        si = (float *)malloc(sr * N * sizeof(float));
+        if (!qi || !si) rc = -3;
+        for (int i = 0; !rc && i < inner; i++) {
+            memcpy(qi + (size_t)(2 * i) * rb, q + (size_t)i * rb, rb);
+            memcpy(qi + (size_t)(2 * i + 1) * rb, q + (size_t)(inner + i) * rb, rb);
+            memcpy(si + (size_t)(2 * i) * sr, sc + (size_t)i * sr, sr * sizeof(float));
+            memcpy(si + (size_t)(2 * i + 1) * sr, sc + (size_t)(inner + i) * sr, sr * sizeof(float));
+        }
+    }
+    memset(out, 0, sizeof *out);
+    out->wtype = dt == ARIA_Q8 ? ARIA_WQ8 : ARIA_WQ4; out->N = N; out->K = K;
+    if (!rc) rc = dalloc(&out->q, rb * N, acc) ? -3 : 0;
+    if (!rc) rc = dalloc((void **)&out->scale, sr * N * sizeof(float), acc) ? -3 : 0;
+    if (!rc && (hipMemcpy(out->q, qi ? qi : q, rb * N, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(out->scale, si ? si : sc, sr * N * sizeof(float), hipMemcpyHostToDevice) != hipSuccess))
+        rc = -3;
+    if (rc) dm_free(out);
+    free(q); free(sc); free(qi); free(si);
+    return rc;
+}
+
+int aria_hip_dit_load_overlay(aria_cuda_dit *h, const char *path) {
+    int rc = aria_hip_ensure();
+    if (rc) return rc;
+    if (!h || !path) { aria_hip_set_error("aria_hip_dit_load_overlay: invalid argument"); return ARIA_HIP_EINVAL; }
+    FILE *f = fopen(path, "rb");
+    if (!f) { aria_hip_set_error("aria_hip_dit_load_overlay: cannot open %s", path); return ARIA_HIP_EINVAL; }
+    char magic[8];
+    int32_t hdr[4];
+    if (ov_read(f, magic, 8) || memcmp(magic, "ARIAQNT1", 8) || ov_read(f, hdr, sizeof hdr) ||
+        (hdr[0] != ARIA_Q8 && hdr[0] != ARIA_Q4) || hdr[1] != h->depth || hdr[2] != h->ed || hdr[3] != h->inner) {
+        fclose(f);
+        aria_hip_set_error("aria_hip_dit_load_overlay: not a packed overlay for this model (depth %d, ed %d, inner %d)",
+                           h->depth, h->ed, h->inner);
+        return ARIA_HIP_EINVAL;
+    }
+    const int ed = h->ed, inner = h->inner;
+    /* read every record first, so a bad file leaves the model as it was */
+    dmat *nw = (dmat *)calloc((size_t)h->depth * 6, sizeof(dmat));
+    rc = nw ? 0 : -3;
+    for (int i = 0; !rc && i < h->depth; i++) {
+        aria_hip_dit_block *b = h->blk[i];
+        const int glu = b->ffn == ARIA_FFN_GLU;
+        const int shp[6][2] = {{3 * ed, ed}, {ed, ed}, {ed, ed}, {ed, ed}, {b->ffrows, ed}, {ed, inner}};
+        for (int j = 0; !rc && j < 6; j++)
+            rc = ov_record(f, shp[j][0], shp[j][1], j == 4 && glu, b->w8, &nw[i * 6 + j], &b->bytes);
+    }
+    fclose(f);
+    if (rc) {
+        if (nw) for (int k = 0; k < h->depth * 6; k++) dm_free(&nw[k]);
+        free(nw);
+        aria_hip_set_error("aria_hip_dit_load_overlay: %s", rc == -3 ? "out of memory"
+                           : rc == -2 ? "record type or shape does not match the model (W8A8 blocks need Q8)"
+                                      : "truncated file");
+        return rc == -3 ? ARIA_HIP_ENOMEM : ARIA_HIP_EINVAL;
+    }
+    /* in-flight steps use the old weights; a captured step holds their addresses */
+    hipStreamSynchronize(h->st);
+    if (h->gexec) hipGraphExecDestroy(h->gexec);
+    if (h->graph) hipGraphDestroy(h->graph);
+    h->gexec = NULL; h->graph = NULL; h->graph_ready = 0; h->graph_failed = 0;
+    for (int i = 0; i < h->depth; i++) {
+        aria_hip_dit_block *b = h->blk[i];
+        dmat *dst[6] = {&b->sa_qkv, &b->sa_out, &b->ca_q, &b->ca_out, &b->ff_in, &b->ff_out};
+        for (int j = 0; j < 6; j++) { dm_free(dst[j]); *dst[j] = nw[i * 6 + j]; }
+        b->prec = (aria_dtype)hdr[0];
+    }
+    free(nw);
+    return 0;
+}
 
 int aria_hip_dit_device_buffers(aria_cuda_dit *h, float **dx, float **dv, float **dgcond) {
     if (!h || !h->have_req) return ARIA_HIP_EINVAL;

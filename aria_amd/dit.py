@@ -265,6 +265,11 @@ class Dit:
     def graph_active(self):
         return bool(lib().aria_hip_dit_graph_active(self.h))
 
+    def load_overlay(self, path):
+        """Take the block GEMM weights from the reference's packed .aria overlay
+        (aria_sa3_dit_quant_save's file) instead of quantising them at create."""
+        check(lib().aria_hip_dit_load_overlay(self.h, str(path).encode()), "aria_hip_dit_load_overlay")
+
     def free(self):
         if self.h:
             lib().aria_cuda_dit_free(self.h)

@@ -175,6 +175,15 @@ int aria_hip_dit_device_buffers(aria_cuda_dit *h, float **dx, float **dv, float 
 int aria_hip_dit_run(aria_cuda_dit *h, void *stream);
 /* 1 if the step runs as a captured graph, 0 if inline */
 int aria_hip_dit_graph_active(const aria_cuda_dit *h);
+/* Load the reference's packed block overlay (.aria: aria_sa3_dit_quant_save's file,
+ * src/aria_sa3_dit.c:509-527, records of aria_qweight_write, src/aria_quant.c:439-449) into the
+ * device model: the six block GEMM weights of every block are taken from the file as packed
+ * (Q8 / Q4 per record) instead of being quantised from the f32 view, so the quantisation at
+ * create is skipped (the reference loads it with aria_sa3_dit_quant_load, src/aria_sa3_dit.c:
+ * 529-551, for its CPU path). depth / ed / inner and every record's shape must match the model;
+ * a W8A8 (ARIA_Q8A8) model needs Q8 records. A captured step is dropped (re-captured on the
+ * next step). 0, or an error with the model unchanged. */
+int aria_hip_dit_load_overlay(aria_cuda_dit *h, const char *path);
 
 /* ---- device decoders (src/aria_sa3_dec.h:98-109): not served by this backend ----
  * create returns NULL (no fit), so the reference's caller keeps its CPU decoder

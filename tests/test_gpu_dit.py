@@ -292,3 +292,82 @@ def test_dit_config5_step(hip, port, R):
         print(f"config-5 step seq {b}: max|d| {d.max():.3e} max|ref| {np.abs(want).max():.3f}", flush=True)
         assert_close(got[b], want, ATOL, RTOL, f"config-5 step seq {b}")
     dit.free()
+
+
+def write_overlay(R, M, path, precision="q4"):
+    """The reference's packed overlay file: the header as aria_sa3_dit_quant_save writes it
+    (src/aria_sa3_dit.c:521-523), every record by the reference's own aria_qweight_write
+    (src/aria_quant.c:439-449) on the reference quantizer's output, in the recipe's types."""
+    import ctypes as C
+    libc = C.CDLL(None)
+    libc.fopen.restype = C.c_void_p
+    libc.fopen.argtypes = [C.c_char_p, C.c_char_p]
+    libc.fwrite.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]
+    libc.fclose.argtypes = [C.c_void_p]
+
+    class QW(C.Structure):   # aria_qweight (src/aria_quant.h:76-83)
+        _fields_ = [("dt", C.c_int), ("N", C.c_int), ("K", C.c_int), ("f32", C.c_void_p), ("q", C.c_void_p),
+                    ("scale", C.c_void_p), ("a8", C.c_int)]
+    R.lib.aria_qweight_write.argtypes = [C.c_void_p, C.c_void_p]
+    R.lib.aria_qweight_write.restype = C.c_int
+    blocks = M["blocks"]
+    ed, inner = M["project_in"].shape[0], blocks[0]["ff_out_w"].shape[1]
+    f = libc.fopen(str(path).encode(), b"wb")
+    assert f
+    keep = []
+    try:
+        libc.fwrite(b"ARIAQNT1", 1, 8, f)
+        hdr = (C.c_int32 * 4)(4 if precision == "q4" else 3, len(blocks), ed, inner)
+        libc.fwrite(hdr, 4, 4, f)
+        for W in blocks:
+            for name in ("sa_to_qkv", "sa_to_out", "ca_to_q", "ca_to_out", "ff_in_w", "ff_out_w"):
+                w = np.ascontiguousarray(W[name], np.float32)
+                if precision == "q4" and name.startswith("ff_"):
+                    q, sc = R.q4_quant(w); dt = 4
+                else:
+                    q, sc = R.q8_quant(w); dt = 3
+                keep += [q, sc]
+                rec = QW(dt, w.shape[0], w.shape[1], None, q.ctypes.data, sc.ctypes.data, 0)
+                assert R.lib.aria_qweight_write(f, C.byref(rec)) == 0
+    finally:
+        libc.fclose(f)
+
+
+def test_dit_packed_overlay(hip, port, R, tmp_path):
+    """aria_hip_dit_load_overlay (F3): the reference's .aria overlay loaded into the device model
+    gives steps bit-identical to the model that packs the same f32 weights on the device (whose
+    pack is bit-exact with the reference quantizer), with the captured step re-made; files that
+    do not fit the model are refused and leave it working."""
+    M = model(19)
+    T, n_cond, H, rot = 24, 8, 2, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = R.rope_freqs(S, rot, 10000.0)
+    path = tmp_path / "dit.aria"
+    write_overlay(R, M, path)
+    a, b = make_dit(M, 4, H, rot), make_dit(M, 4, H, rot)
+    _, ced, _ = inputs(5, 1, io_ch, T, n_cond, ed)
+    x, _, g = inputs(300, 1, io_ch, T, n_cond, ed)
+    for d in (a, b):
+        d.set_request(T, [ced[0]], c, s)
+    y0 = b.step(x, g)                                      # captures b's step
+    b.load_overlay(path)
+    ya, yb = a.step(x, g), b.step(x, g)
+    assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)) and np.array_equal(ya.view(np.uint32), y0.view(np.uint32))
+    # another model's file (depth differs) and a Q4 file for a W8A8 model are refused
+    M3 = model(20, depth=3)
+    bad = tmp_path / "depth3.aria"
+    write_overlay(R, M3, bad)
+    L = hip.lib()
+    assert L.aria_hip_dit_load_overlay(b.h, str(bad).encode()) == -1
+    assert np.array_equal(b.step(x, g).view(np.uint32), yb.view(np.uint32))
+    M8 = model(21, ed=256, inner=512)
+    w8 = make_dit(M8, 5, 4, rot)
+    q4file = tmp_path / "q4.aria"
+    write_overlay(R, M8, q4file)
+    assert L.aria_hip_dit_load_overlay(w8.h, str(q4file).encode()) == -1
+    q8file = tmp_path / "q8.aria"
+    write_overlay(R, M8, q8file, "q8")
+    assert L.aria_hip_dit_load_overlay(w8.h, str(q8file).encode()) == 0
+    for d in (a, b, w8):
+        d.free()
