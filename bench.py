@@ -414,8 +414,10 @@ def dit_leg(DeviceArray, Timer, L, chk, stream, rng, steps=8, depth=24):
     convs [64,64]; context embeddings [2, 256, 1024] ~N(0,1) (cross K/V projected once per
     request, outside the timing); per-step gcond [2, 6*1024] ~N(0,0.1). Timed: 8 device-resident
     steps (aria_hip_dit_run) replaying the captured graph, the same with the graph off, and the
-    whole 8-step pingpong sampler (aria_cuda_dit_sample: host noise + H2D each step)."""
-    from aria_amd.dit import Dit, random_dit, FFN_GELU, Q4
+    whole 8-step pingpong sampler (aria_cuda_dit_sample: host noise + H2D each step).
+    graph_w8a8_*: the same stack and steps in W8A8 mode (ARIA_Q8A8, what --precision auto picks
+    on gfx950), graph replay."""
+    from aria_amd.dit import Dit, random_dit, FFN_GELU, Q4, Q8A8
     Bb, T, C, ed, H, inner, Sc = B, S, 64, 1024, 16, 4096, 256
     M = random_dit(rng, depth, ed, inner, C, 0, ffn=FFN_GELU)
     inv = 1.0 / (10000.0 ** (np.arange(16) * 2.0 / 32))
@@ -426,11 +428,12 @@ def dit_leg(DeviceArray, Timer, L, chk, stream, rng, steps=8, depth=24):
     gall = (0.1 * rng.standard_normal((steps, Bb, 6 * ed))).astype(np.float32)
     sched = np.linspace(1.0, 0.0, steps + 1).astype(np.float32)
     out = {"depth": depth, "T": T, "batch": Bb, "io_ch": C, "steps": steps, "ffn": "gelu4x", "precision": "q4"}
-    for mode in ("graph", "inline"):
+    for mode in ("graph", "inline", "graph_w8a8"):
         if mode == "inline":
             os.environ["ARIA_NO_GRAPH"] = "1"
         try:
-            dit = Dit(M, depth, ed, H, inner, C, 0, 32, precision=Q4, ffn=FFN_GELU)
+            dit = Dit(M, depth, ed, H, inner, C, 0, 32, precision=Q8A8 if mode == "graph_w8a8" else Q4,
+                      ffn=FFN_GELU)
         finally:
             os.environ.pop("ARIA_NO_GRAPH", None)
         dit.set_request(T, ced, cos32, sin32)
