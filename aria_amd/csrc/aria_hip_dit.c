@@ -129,11 +129,7 @@ aria_hip_dit_block *aria_hip_dit_block_create(const aria_dit_block_w *w, int dim
                            dim, num_heads, head_dim, inner, dim_ctx);
         return NULL;
     }
-    if (precision == ARIA_Q8A8 && dim != 256 && dim != 512 && dim != 768 && dim != 1024 && dim != 2048) {
-        /* the W8A8 norms quantise rows held in registers (k_rownorm's register path) */
-        aria_hip_set_error("aria_hip_dit_block_create: W8A8 needs dim 256, 512, 768, 1024 or 2048 (got %d)", dim);
-        return NULL;
-    }
+
     aria_hip_dit_block *b = (aria_hip_dit_block *)calloc(1, sizeof *b);
     if (!b) return NULL;
     b->dim = dim; b->H = num_heads; b->hd = head_dim; b->inner = inner; b->ffn = ffn; b->dim_ctx = dim_ctx;
@@ -321,15 +317,26 @@ static hipError_t gemm_i8(const dmat *m, float *y, const wsl *w, const float *bi
  * scales directly, and the attention outputs and the FFN product, whose rows span many
  * workgroups, are written fp32 and quantised by aria_k_quant_act_q8. The int8 GEMMs carry the
  * same fused epilogues (heads, gated residual, residual + local cond, GLU / GELU). */
+/* the widths whose rows the norm kernel holds in registers (and can quantise there) */
+static int w8_fused_norm(int d) { return d == 256 || d == 512 || d == 768 || d == 1024 || d == 2048; }
+
 static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int B, int S, const float *const *tc,
                             const float *const *gc, int gbs, const uint16_t *dk, const uint16_t *dv, int Sc,
                             const float *dcos, const float *dsin, int rot, const float *dlocal, hipStream_t s) {
     const int d = b->dim, H = b->H, M = B * S;
     const float eps_norm = 1e-5f, eps_qk = 1e-6f;
 
+    const int fused = w8_fused_norm(d);   /* else: fp32 norm, then the quantiser */
+
     /* ---- self-attention ---- */
-    STEP(aria_k_rownorm_ada_q8(w->xq, w->sx, dx, b->pre_norm, tc[0], tc[1], gc[0], gc[1], gbs, S, M, d, eps_norm, s),
-         "k_rownorm_q8 (pre_norm + adaLN)");
+    if (fused) {
+        STEP(aria_k_rownorm_ada_q8(w->xq, w->sx, dx, b->pre_norm, tc[0], tc[1], gc[0], gc[1], gbs, S, M, d, eps_norm, s),
+             "k_rownorm_q8 (pre_norm + adaLN)");
+    } else {
+        STEP(aria_k_rownorm_ada(w->f32, 0, dx, b->pre_norm, tc[0], tc[1], gc[0], gc[1], gbs, S, M, d, eps_norm, s),
+             "k_rownorm (pre_norm + adaLN)");
+        STEP(aria_k_quant_act_q8(w->xq, w->sx, w->f32, 0, M, d, s), "k_quant_act_q8 (pre_norm)");
+    }
     {
         const int kind[3] = {0, 1, 2};
         uint16_t *dst[3] = {w->q16, w->k16, w->v16};
@@ -345,8 +352,14 @@ static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int 
     }
 
     /* ---- cross-attention ---- */
-    STEP(aria_k_rownorm_q8(w->xq, w->sx, dx, b->cross_norm, NULL, NULL, 0, M, d, eps_norm, s),
-         "k_rownorm_q8 (cross_norm)");
+    if (fused) {
+        STEP(aria_k_rownorm_q8(w->xq, w->sx, dx, b->cross_norm, NULL, NULL, 0, M, d, eps_norm, s),
+             "k_rownorm_q8 (cross_norm)");
+    } else {
+        STEP(aria_k_rownorm(w->f32, 0, dx, b->cross_norm, NULL, NULL, NULL, 0, 0, 0, ARIA_NORM_RMS, M, d, eps_norm, s),
+             "k_rownorm (cross_norm)");
+        STEP(aria_k_quant_act_q8(w->xq, w->sx, w->f32, 0, M, d, s), "k_quant_act_q8 (cross_norm)");
+    }
     {
         const int kind[1] = {0};
         uint16_t *dst[1] = {w->q16};
@@ -362,8 +375,14 @@ static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int 
     }
 
     /* ---- feed-forward ---- */
-    STEP(aria_k_rownorm_ada_q8(w->xq, w->sx, dx, b->ff_norm, tc[3], tc[4], gc[3], gc[4], gbs, S, M, d, eps_norm, s),
-         "k_rownorm_q8 (ff_norm + adaLN)");
+    if (fused) {
+        STEP(aria_k_rownorm_ada_q8(w->xq, w->sx, dx, b->ff_norm, tc[3], tc[4], gc[3], gc[4], gbs, S, M, d, eps_norm, s),
+             "k_rownorm_q8 (ff_norm + adaLN)");
+    } else {
+        STEP(aria_k_rownorm_ada(w->f32, 0, dx, b->ff_norm, tc[3], tc[4], gc[3], gc[4], gbs, S, M, d, eps_norm, s),
+             "k_rownorm (ff_norm + adaLN)");
+        STEP(aria_k_quant_act_q8(w->xq, w->sx, w->f32, 0, M, d, s), "k_quant_act_q8 (ff_norm)");
+    }
     if (b->ffn == ARIA_FFN_GLU) {
         aria_qgemm_epi e;
         memset(&e, 0, sizeof e);

@@ -89,6 +89,17 @@ def test_block_config4_full(hip, port, R, ffn):
     assert_close(got, want, ATOL, RTOL, f"config-4 block ffn={ffn}")
 
 
+def test_block_w8a8_other_width(hip, port, R):
+    """W8A8 at a model width the norm kernel does not hold in registers (384): fp32 norm, then
+    the per-row quantiser (the reference's order exactly), same gate as the small blocks."""
+    B, S, Sc, dim, H, inner, dim_ctx = 2, 40, 16, 384, 6, 768, 64
+    W, x, ctx, gcond = case(55, B, S, Sc, dim, inner, dim_ctx, 0)
+    c, s = R.rope_freqs(S, 32, 10000.0)
+    got = run_block(W, x, ctx, gcond, H, inner, dim_ctx, 0, 5, 32, c, s)
+    want = reference_blocks(R, port, W, x, ctx, gcond, H, inner, "q8a8", 32, c, s, 0)
+    assert_close(got, want, ATOL, RTOL, "block q8a8 dim 384")
+
+
 # W8A8 gate at full size: the int8 activation rounding (one step = 1/127 of the row max)
 # amplifies the fp16 attention's ~1e-3 difference from the fp32 oracle: ~3 % of the quantised
 # attention outputs land one step away, ~0.5 % of the out-projection (measured rms 2.8e-3,

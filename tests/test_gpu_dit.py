@@ -95,8 +95,8 @@ def test_dit_step_parity(hip, port, R, precision):
 
 
 def test_dit_step_parity_w8a8(hip, port, R):
-    """aria_cuda_dit_step with ARIA_Q8A8 (int8 activations on every Q8 projection; the W8A8
-    norms need ed >= 256): against the composition of reference ops with aria_linear_q8a8."""
+    """aria_cuda_dit_step with ARIA_Q8A8 (int8 activations on every Q8 projection; at ed 256 the
+    norms quantise in registers): against the composition of reference ops with aria_linear_q8a8."""
     M = model(17, ed=256, inner=512)
     T, n_cond, H, rot = 40, 12, 4, 32
     io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
