@@ -145,7 +145,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is design-only "
-                                   "(see DESIGN.md). Run with --gpus 1."}))
+                                   "(one process per GPU, each the N = 1 path on its own rows). Run with --gpus 1."}))
         sys.exit(2)
 
     import aria_amd
