@@ -104,6 +104,15 @@ static int pack(dmat *m, const float *W, int N, int K, int wtype, hipStream_t s,
     return e == hipSuccess ? 0 : FAIL(e, "block weight packing");
 }
 
+/* device bytes of a packed matrix, as pack() and the overlay loader allocate them */
+static size_t dm_bytes(const dmat *m) {
+    if (!m->q) return 0;
+    const size_t N = (size_t)m->N, K = (size_t)m->K;
+    if (m->wtype == ARIA_WQ8) return N * K + N * 4;
+    if (m->wtype == ARIA_WQ4) return N * ((K + 1) / 2) + N * 2 * ((K + 31) / 32) * 4;
+    return N * K * 2;
+}
+
 static void dm_free(dmat *m) {
     dfree(m->q);
     dfree(m->scale);
@@ -483,6 +492,36 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
 /* device-resident DiT (the reference's aria_cuda_dit_* ABI)                 */
 /* ------------------------------------------------------------------------- */
 
+/* A growable staging buffer: device memory or pinned host memory. Its contents do not
+ * survive a grow. */
+typedef struct {
+    void *p;
+    size_t cap;
+} sbuf;
+
+static int sbuf_reserve(sbuf *b, size_t bytes, int pinned) {
+    if (bytes <= b->cap) return 0;
+    if (b->p) {
+        if (pinned) hipHostFree(b->p); else hipFree(b->p);
+    }
+    b->p = NULL; b->cap = 0;
+    const size_t want = bytes + bytes / 4;  /* slack, so a slightly longer request reuses it */
+    hipError_t e = pinned ? hipHostMalloc(&b->p, want, 0) : hipMalloc(&b->p, want);
+    if (e != hipSuccess) { hipGetLastError(); b->p = NULL; return -1; }
+    b->cap = want;
+    return 0;
+}
+
+static void sbuf_release(sbuf *b, int pinned) {
+    if (b->p) {
+        if (pinned) hipHostFree(b->p); else hipFree(b->p);
+    }
+    b->p = NULL; b->cap = 0;
+}
+
+enum { GRAPH_NONE = 0, GRAPH_LIVE = 1, GRAPH_OFF = 2 };
+#define NZ_SLOTS 2
+
 struct aria_cuda_dit {
     int depth, ed, H, inner, io_ch, n_mem, rot;
     aria_hip_dit_block **blk;
@@ -497,14 +536,18 @@ struct aria_cuda_dit {
     float *saved_ced;                       /* host copy of the B context embeddings */
     void *ws;
     size_t ws_bytes;
-    float *dx, *dv, *dgcond, *dxtc, *dtmp, *dseq, *dout, *dnoise;
-    /* captured step */
+    float *dx, *dv, *dgcond, *dxtc, *dtmp, *dseq, *dout;
+    /* the step as a HIP graph (see graph_ensure) */
+    int gstate;                             /* GRAPH_NONE / GRAPH_LIVE / GRAPH_OFF */
+    int no_graph;                           /* ARIA_NO_GRAPH at create: inline for good */
     hipGraph_t graph;
     hipGraphExec_t gexec;
-    int graph_ready, graph_failed, no_graph;
-    /* pinned staging for the sampler */
-    float *pin_gc, *pin_nz[2];
-    size_t pin_gc_n, pin_nz_n;
+    /* sampler staging (see aria_cuda_dit_sample) */
+    sbuf gc_tab;                            /* device: every step's gcond rows */
+    sbuf nz_host, nz_dev;                   /* NZ_SLOTS noise slots, pinned host / device */
+    hipStream_t up;                         /* upload stream for the noise slots */
+    hipEvent_t ev_up[NZ_SLOTS], ev_used[NZ_SLOTS], ev_step;
+    int have_events;
 };
 
 static int up_mat(float **d, const float *h, size_t n) {
@@ -513,17 +556,24 @@ static int up_mat(float **d, const float *h, size_t n) {
     return upv(d, h, n, NULL);
 }
 
-static void req_free(aria_cuda_dit *h) {
+/* forget the captured step (buffers or weights it names are about to change); the next
+ * run captures again unless the handle is inline for good */
+static void graph_drop(aria_cuda_dit *h) {
     if (h->gexec) hipGraphExecDestroy(h->gexec);
     if (h->graph) hipGraphDestroy(h->graph);
-    h->gexec = NULL; h->graph = NULL; h->graph_ready = 0; h->graph_failed = 0;
+    h->gexec = NULL; h->graph = NULL;
+    h->gstate = h->no_graph ? GRAPH_OFF : GRAPH_NONE;
+}
+
+static void req_free(aria_cuda_dit *h) {
+    graph_drop(h);
     if (h->ck) for (int b = 0; b < h->depth; b++) { dfree(h->ck[b]); dfree(h->cv[b]); }
     if (h->local) for (int b = 0; b < h->depth; b++) dfree(h->local[b]);
     free(h->ck); free(h->cv); free(h->local);
     h->ck = h->cv = NULL; h->local = NULL;
-    float *bufs[] = {h->cos_t, h->sin_t, h->dx, h->dv, h->dgcond, h->dxtc, h->dtmp, h->dseq, h->dout, h->dnoise};
+    float *bufs[] = {h->cos_t, h->sin_t, h->dx, h->dv, h->dgcond, h->dxtc, h->dtmp, h->dseq, h->dout};
     for (size_t i = 0; i < sizeof bufs / sizeof *bufs; i++) dfree(bufs[i]);
-    h->cos_t = h->sin_t = h->dx = h->dv = h->dgcond = h->dxtc = h->dtmp = h->dseq = h->dout = h->dnoise = NULL;
+    h->cos_t = h->sin_t = h->dx = h->dv = h->dgcond = h->dxtc = h->dtmp = h->dseq = h->dout = NULL;
     dfree(h->ws);
     h->ws = NULL; h->ws_bytes = 0;
     free(h->saved_ced);
@@ -539,9 +589,15 @@ void aria_cuda_dit_free(aria_cuda_dit *h) {
     free(h->blk);
     float *w[] = {h->pre, h->post, h->pin, h->pout, h->mem};
     for (size_t i = 0; i < sizeof w / sizeof *w; i++) dfree(w[i]);
-    if (h->pin_gc) hipHostFree(h->pin_gc);
-    if (h->pin_nz[0]) hipHostFree(h->pin_nz[0]);
-    if (h->pin_nz[1]) hipHostFree(h->pin_nz[1]);
+    if (h->up) hipStreamSynchronize(h->up);
+    sbuf_release(&h->gc_tab, 0);
+    sbuf_release(&h->nz_dev, 0);
+    sbuf_release(&h->nz_host, 1);
+    if (h->have_events) {
+        for (int i = 0; i < NZ_SLOTS; i++) { hipEventDestroy(h->ev_up[i]); hipEventDestroy(h->ev_used[i]); }
+        hipEventDestroy(h->ev_step);
+    }
+    if (h->up) hipStreamDestroy(h->up);
     if (h->st) hipStreamDestroy(h->st);
     free(h);
 }
@@ -555,12 +611,16 @@ aria_cuda_dit *aria_hip_dit_create_ex(const aria_sa3_dit_view *v, aria_dtype pre
     }
     /* auto: W8A8 where the int8 matrix path exists, as the reference (src/aria_model_sa3.c:500-502) */
     if (precision == ARIA_DTYPE_AUTO) precision = aria_cuda_int8_tc() ? ARIA_Q8A8 : ARIA_F32;
+    /* ARIA_W8A8 set (any value) turns a Q8 model into W8A8, the reference's opt-in knob
+     * (src/aria_cuda.cu:1186, and aria_linear_qw on the CPU, src/aria_quant.c:420-421) */
+    if (precision == ARIA_Q8 && getenv("ARIA_W8A8") != NULL) precision = ARIA_Q8A8;
     aria_cuda_dit *h = (aria_cuda_dit *)calloc(1, sizeof *h);
     if (!h) return NULL;
     h->depth = v->depth; h->ed = v->ed; h->H = v->num_heads; h->inner = v->inner; h->io_ch = v->io_ch;
     h->n_mem = v->n_mem; h->rot = v->rot_dim;
     const char *ng = getenv("ARIA_NO_GRAPH");   /* read once per handle */
     h->no_graph = ng && ng[0] && ng[0] != '0';
+    h->gstate = h->no_graph ? GRAPH_OFF : GRAPH_NONE;
     if (hipStreamCreateWithFlags(&h->st, hipStreamNonBlocking) != hipSuccess) { free(h); return NULL; }
     /* VRAM fit: packed blocks (<= fp16 size) + fp32 io projections, with margin */
     size_t fr = 0, tot = 0;
@@ -633,7 +693,7 @@ static int req_setup(aria_cuda_dit *h, const aria_sa3_dit_req_view *rv, int B) {
     rc = dalloc(&h->ws, need, NULL);
     h->ws_bytes = need;
     const size_t nxc = (size_t)B * C * T;
-    float **step_bufs[] = {&h->dx, &h->dv, &h->dxtc, &h->dtmp, &h->dout, &h->dnoise};
+    float **step_bufs[] = {&h->dx, &h->dv, &h->dxtc, &h->dtmp, &h->dout};
     for (size_t i = 0; i < sizeof step_bufs / sizeof *step_bufs && !rc; i++)
         rc = dalloc((void **)step_bufs[i], nxc * 4, NULL);
     if (!rc) rc = dalloc((void **)&h->dgcond, (size_t)B * 6 * E * 4, NULL);
@@ -754,38 +814,41 @@ static int step_compute(aria_cuda_dit *h, hipStream_t s) {
     return 0;
 }
 
-/* run one step: replay the captured graph, capturing it on first use (ARIA_NO_GRAPH=1 when the
- * handle was created, or a failed capture -> inline; the reference's policy,
- * src/aria_cuda.cu:1450-1489) */
-static int dit_run(aria_cuda_dit *h, hipStream_t s) {
-    if (h->no_graph) h->graph_failed = 1;
-    if (h->graph_ready) {
-        hipError_t e = hipGraphLaunch(h->gexec, s);
-        return e == hipSuccess ? 0 : FAIL(e, "hipGraphLaunch");
-    }
-    if (h->graph_failed) return step_compute(h, s);
-    hipStreamSynchronize(s);
-    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+/* The step as one HIP graph, captured from the handle's stream the first time a step runs
+ * on the current request's buffers and replayed from then on; set_request (for a new layout)
+ * and an overlay load drop it. Capture is thread-local, so work that other threads enqueue
+ * meanwhile is not pulled in. If capture or instantiation fails the handle runs the kernels
+ * inline from then on, with the same results. Returns 1 when a graph is ready. */
+static int graph_ensure(aria_cuda_dit *h) {
+    if (h->gstate != GRAPH_NONE) return h->gstate == GRAPH_LIVE;
+    h->gstate = GRAPH_OFF;   /* unless everything below succeeds */
+    if (hipStreamSynchronize(h->st) != hipSuccess ||
+        hipStreamBeginCapture(h->st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
         hipGetLastError();
-        h->graph_failed = 1;
-        return step_compute(h, s);
+        return 0;
     }
-    int rc = step_compute(h, s);
+    const int rc = step_compute(h, h->st);
     hipGraph_t g = NULL;
-    hipError_t e = hipStreamEndCapture(s, &g);
-    if (!rc && e == hipSuccess && g && hipGraphInstantiate(&h->gexec, g, NULL, NULL, 0) == hipSuccess) {
-        h->graph = g;
-        h->graph_ready = 1;
-        e = hipGraphLaunch(h->gexec, s);
-        return e == hipSuccess ? 0 : FAIL(e, "hipGraphLaunch");
+    hipGraphExec_t x = NULL;
+    const hipError_t ec = hipStreamEndCapture(h->st, &g);
+    if (rc || ec != hipSuccess || !g || hipGraphInstantiate(&x, g, NULL, NULL, 0) != hipSuccess) {
+        hipGetLastError();
+        if (g) hipGraphDestroy(g);
+        return 0;
     }
-    hipGetLastError();
-    if (g) hipGraphDestroy(g);
-    h->graph_failed = 1;
-    return step_compute(h, s);   /* capture failed: run inline (correctness preserved) */
+    h->graph = g;
+    h->gexec = x;
+    h->gstate = GRAPH_LIVE;
+    return 1;
 }
 
-int aria_hip_dit_graph_active(const aria_cuda_dit *h) { return h && h->graph_ready; }
+static int dit_run(aria_cuda_dit *h, hipStream_t s) {
+    if (!graph_ensure(h)) return step_compute(h, s);
+    const hipError_t e = hipGraphLaunch(h->gexec, s);
+    return e == hipSuccess ? 0 : FAIL(e, "hipGraphLaunch");
+}
+
+int aria_hip_dit_graph_active(const aria_cuda_dit *h) { return h && h->gstate == GRAPH_LIVE; }
 
 /* ---- the reference's packed DiT overlay (.aria) ----
  * File (aria_sa3_dit_quant_save, src/aria_sa3_dit.c:509-527): "ARIAQNT1", int32 {dt, depth, ed,
@@ -852,18 +915,20 @@ int aria_hip_dit_load_overlay(aria_cuda_dit *h, const char *path) {
     const int ed = h->ed, inner = h->inner;
     /* read every record first, so a bad file leaves the model as it was */
     dmat *nw = (dmat *)calloc((size_t)h->depth * 6, sizeof(dmat));
-    rc = nw ? 0 : -3;
+    size_t *nbytes = (size_t *)calloc((size_t)h->depth, sizeof(size_t));   /* new bytes per block */
+    rc = nw && nbytes ? 0 : -3;
     for (int i = 0; !rc && i < h->depth; i++) {
         aria_hip_dit_block *b = h->blk[i];
         const int glu = b->ffn == ARIA_FFN_GLU;
         const int shp[6][2] = {{3 * ed, ed}, {ed, ed}, {ed, ed}, {ed, ed}, {b->ffrows, ed}, {ed, inner}};
         for (int j = 0; !rc && j < 6; j++)
-            rc = ov_record(f, shp[j][0], shp[j][1], j == 4 && glu, b->w8, &nw[i * 6 + j], &b->bytes);
+            rc = ov_record(f, shp[j][0], shp[j][1], j == 4 && glu, b->w8, &nw[i * 6 + j], &nbytes[i]);
     }
     fclose(f);
     if (rc) {
         if (nw) for (int k = 0; k < h->depth * 6; k++) dm_free(&nw[k]);
         free(nw);
+        free(nbytes);
         aria_hip_set_error("aria_hip_dit_load_overlay: %s", rc == -3 ? "out of memory"
                            : rc == -2 ? "record type or shape does not match the model (W8A8 blocks need Q8)"
                                       : "truncated file");
@@ -871,16 +936,20 @@ int aria_hip_dit_load_overlay(aria_cuda_dit *h, const char *path) {
     }
     /* in-flight steps use the old weights; a captured step holds their addresses */
     hipStreamSynchronize(h->st);
-    if (h->gexec) hipGraphExecDestroy(h->gexec);
-    if (h->graph) hipGraphDestroy(h->graph);
-    h->gexec = NULL; h->graph = NULL; h->graph_ready = 0; h->graph_failed = 0;
+    graph_drop(h);
     for (int i = 0; i < h->depth; i++) {
         aria_hip_dit_block *b = h->blk[i];
         dmat *dst[6] = {&b->sa_qkv, &b->sa_out, &b->ca_q, &b->ca_out, &b->ff_in, &b->ff_out};
-        for (int j = 0; j < 6; j++) { dm_free(dst[j]); *dst[j] = nw[i * 6 + j]; }
+        for (int j = 0; j < 6; j++) {
+            b->bytes -= dm_bytes(dst[j]);
+            dm_free(dst[j]);
+            *dst[j] = nw[i * 6 + j];
+        }
+        b->bytes += nbytes[i];
         b->prec = (aria_dtype)hdr[0];
     }
     free(nw);
+    free(nbytes);
     return 0;
 }
 
@@ -921,55 +990,73 @@ void aria_cuda_dit_step(aria_cuda_dit *h, float *v_CT, const float *x_CT, const 
     aria_hip_dit_step_batch(h, v_CT, x_CT, gcond);
 }
 
-static int pin_grow(float **p, size_t *cap, size_t n) {
-    if (n <= *cap) return 0;
-    if (*p) hipHostFree(*p);
-    *p = NULL; *cap = 0;
-    if (hipHostMalloc((void **)p, n * sizeof(float), 0) != hipSuccess) { hipGetLastError(); *p = NULL; return -1; }
-    *cap = n;
+/* Sampler staging, reserved before the first step runs: the gcond table of every step on the
+ * device, NZ_SLOTS noise slots in pinned host memory and on the device, an upload stream and
+ * the slot events. -1 leaves the handle as it was for the step path. */
+static int sample_stage(aria_cuda_dit *h, int steps, size_t n, size_t ng) {
+    if (sbuf_reserve(&h->gc_tab, (size_t)(steps > 0 ? steps : 1) * ng * sizeof(float), 0) ||
+        sbuf_reserve(&h->nz_host, (size_t)NZ_SLOTS * n * sizeof(float), 1) ||
+        sbuf_reserve(&h->nz_dev, (size_t)NZ_SLOTS * n * sizeof(float), 0))
+        return -1;
+    if (!h->up && hipStreamCreateWithFlags(&h->up, hipStreamNonBlocking) != hipSuccess) {
+        hipGetLastError();
+        h->up = NULL;
+        return -1;
+    }
+    if (!h->have_events) {
+        int ok = hipEventCreateWithFlags(&h->ev_step, hipEventDisableTiming) == hipSuccess;
+        for (int i = 0; i < NZ_SLOTS && ok; i++)
+            ok = hipEventCreateWithFlags(&h->ev_up[i], hipEventDisableTiming) == hipSuccess &&
+                 hipEventCreateWithFlags(&h->ev_used[i], hipEventDisableTiming) == hipSuccess;
+        if (!ok) { hipGetLastError(); return -1; }   /* (a partial set is not reused) */
+        h->have_events = 1;
+    }
     return 0;
 }
 
+/* The pingpong sampler with x resident in HBM (contract: src/aria_sa3_dit.h:163-171; the host
+ * loop it reproduces bit for bit is src/aria_sampler.c:203-229).
+ * Per step i on the handle's stream: gcond row i is copied from the device table (uploaded
+ * once, before the first step), the velocity step runs (graph replay), then the update
+ * x = (1 - tn)(x - tc v) + tn noise_i. The host draws noise_i while step i runs, into slot
+ * i % NZ_SLOTS; the slot goes to the device on the upload stream, overlapping the step, and
+ * the update waits for that upload. A slot is refilled only after the update that read its
+ * previous contents (ev_used), which also orders the refill after the slot's last upload.
+ * noise is called exactly once per step, in step order. */
 int aria_cuda_dit_sample(aria_cuda_dit *h, float *x_CT, const float *sched, int steps, const float *gcond_all,
                          void (*noise)(float *, int, void *), void *noise_user, void (*progress)(int, int, void *),
                          void *progress_user) {
     if (aria_hip_ensure() || !h || !h->have_req || !x_CT || !sched || !gcond_all || !noise || steps < 0) return -1;
     const size_t n = (size_t)h->B * h->io_ch * h->T, ng = (size_t)h->B * 6 * h->ed;
-    hipStream_t st = h->st;
-    if (pin_grow(&h->pin_gc, &h->pin_gc_n, (size_t)(steps ? steps : 1) * ng)) return -1;
-    if (h->pin_nz_n < n) {   /* the two noise buffers grow together */
-        size_t c0 = 0, c1 = 0;
-        h->pin_nz_n = 0;
-        if (pin_grow(&h->pin_nz[0], &c0, n) || pin_grow(&h->pin_nz[1], &c1, n)) return -1;
-        h->pin_nz_n = n;
-    }
-    memcpy(h->pin_gc, gcond_all, (size_t)steps * ng * sizeof(float));
-    hipEvent_t ev_nz[2], ev_step;
-    hipEventCreateWithFlags(&ev_nz[0], hipEventDisableTiming);
-    hipEventCreateWithFlags(&ev_nz[1], hipEventDisableTiming);
-    hipEventCreateWithFlags(&ev_step, hipEventDisableTiming);
-    int rc = 0;
-    if (hipMemcpyAsync(h->dx, x_CT, n * 4, hipMemcpyHostToDevice, st) != hipSuccess) rc = -1;
-    for (int i = 0; i < steps && !rc; i++) {
+    if (sample_stage(h, steps, n, ng)) return -1;
+    hipStream_t cs = h->st;
+    float *gtab = (float *)h->gc_tab.p, *hslot = (float *)h->nz_host.p, *dslot = (float *)h->nz_dev.p;
+    int ok = hipMemcpyAsync(h->dx, x_CT, n * 4, hipMemcpyHostToDevice, cs) == hipSuccess &&
+             (steps == 0 || hipMemcpyAsync(gtab, gcond_all, (size_t)steps * ng * 4, hipMemcpyHostToDevice, cs) ==
+                                hipSuccess);
+    for (int i = 0; i < steps && ok; i++) {
+        const int k = i % NZ_SLOTS;
+        float *hk = hslot + (size_t)k * n, *dk = dslot + (size_t)k * n;
         h->cur_step = i;
-        if (hipMemcpyAsync(h->dgcond, h->pin_gc + (size_t)i * ng, ng * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
-            dit_run(h, st)) { rc = -1; break; }
-        const int b = i & 1;
-        if (i >= 2) hipEventSynchronize(ev_nz[b]);      /* step i-2's upload from this buffer is done */
-        noise(h->pin_nz[b], (int)n, noise_user);         /* drawn on the host while the step runs */
-        if (hipMemcpyAsync(h->dnoise, h->pin_nz[b], n * 4, hipMemcpyHostToDevice, st) != hipSuccess) { rc = -1; break; }
-        hipEventRecord(ev_nz[b], st);
-        if (aria_k_pingpong(h->dx, h->dv, h->dnoise, sched[i], sched[i + 1], n, st) != hipSuccess) { rc = -1; break; }
-        if (progress) {
-            hipEventRecord(ev_step, st);
-            hipEventSynchronize(ev_step);
-            progress(i + 1, steps, progress_user);
+        ok = hipMemcpyAsync(h->dgcond, gtab + (size_t)i * ng, ng * 4, hipMemcpyDeviceToDevice, cs) == hipSuccess &&
+             dit_run(h, cs) == 0;
+        if (!ok) break;
+        if (i >= NZ_SLOTS && hipEventSynchronize(h->ev_used[k]) != hipSuccess) { ok = 0; break; }
+        noise(hk, (int)n, noise_user);
+        ok = hipMemcpyAsync(dk, hk, n * 4, hipMemcpyHostToDevice, h->up) == hipSuccess &&
+             hipEventRecord(h->ev_up[k], h->up) == hipSuccess && hipStreamWaitEvent(cs, h->ev_up[k], 0) == hipSuccess &&
+             aria_k_pingpong(h->dx, h->dv, dk, sched[i], sched[i + 1], n, cs) == hipSuccess &&
+             hipEventRecord(h->ev_used[k], cs) == hipSuccess;
+        if (ok && progress) {
+            ok = hipEventRecord(h->ev_step, cs) == hipSuccess && hipEventSynchronize(h->ev_step) == hipSuccess;
+            if (ok) progress(i + 1, steps, progress_user);
         }
     }
-    if (!rc && hipMemcpyAsync(x_CT, h->dx, n * 4, hipMemcpyDeviceToHost, st) != hipSuccess) rc = -1;
-    if (hipStreamSynchronize(st) != hipSuccess) rc = -1;
-    hipEventDestroy(ev_nz[0]); hipEventDestroy(ev_nz[1]); hipEventDestroy(ev_step);
-    return rc;
+    if (ok) ok = hipMemcpyAsync(x_CT, h->dx, n * 4, hipMemcpyDeviceToHost, cs) == hipSuccess;
+    if (hipStreamSynchronize(cs) != hipSuccess) ok = 0;
+    if (hipStreamSynchronize(h->up) != hipSuccess) ok = 0;
+    if (!ok) hipGetLastError();
+    return ok ? 0 : -1;
 }
 
 /* ------------------------------------------------------------------------- */

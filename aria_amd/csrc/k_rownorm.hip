@@ -291,7 +291,10 @@ static bool launch_v(const NormArgs &a, int epi, hipStream_t s, std::integer_seq
 template <int NORM>
 static hipError_t launch_norm(const NormArgs &a, hipStream_t s) {
     const int dim = a.dim;
-    const bool vec = (dim % 4 == 0) && al16(a.x) && (a.f16 ? ((uintptr_t)a.y & 7u) == 0 : al16(a.y)) &&
+    /* y alignment per output form: fp32 float4 stores (16 B), fp16 (8 B), int8 (one uint32 of
+     * four values per lane: 4 B) */
+    const bool yal = a.sx ? ((uintptr_t)a.y & 3u) == 0 : a.f16 ? ((uintptr_t)a.y & 7u) == 0 : al16(a.y);
+    const bool vec = (dim % 4 == 0) && al16(a.x) && yal &&
                      (!a.w || al16(a.w)) && (!a.b || al16(a.b)) && (!a.scale || al16(a.scale)) &&
                      (!a.shift || al16(a.shift)) && (!a.scale_add || al16(a.scale_add)) &&
                      (!a.shift_add || al16(a.shift_add)) && a.mod_bs % 4 == 0 && a.add_bs % 4 == 0;

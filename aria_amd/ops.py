@@ -191,6 +191,42 @@ def add(a, b):
     return y
 
 
+def addto(y, a):
+    """aria_addto (src/aria_ops.h:167): y += a, as aria_hip_add_dev with y aliasing its first input"""
+    from .device import DeviceArray
+    dy = DeviceArray.from_host(_f32(y)); da = DeviceArray.from_host(_f32(a))
+    try:
+        check(lib().aria_hip_add_dev(dy.p, dy.p, da.p, dy.nbytes // 4, None), "aria_hip_add_dev")
+        check(lib().aria_hip_stream_sync(None), "aria_hip_add_dev")
+        return dy.to_host()
+    finally:
+        dy.free(); da.free()
+
+
+def scale(x, s):
+    """aria_scale (src/aria_ops.h:168): y = x * s (returns y)"""
+    from .device import DeviceArray
+    dx = DeviceArray.from_host(_f32(x)); dy = DeviceArray(dx.shape)
+    try:
+        check(lib().aria_hip_scale_dev(dy.p, dx.p, s, dx.nbytes // 4, None), "aria_hip_scale_dev")
+        check(lib().aria_hip_stream_sync(None), "aria_hip_scale_dev")
+        return dy.to_host()
+    finally:
+        dx.free(); dy.free()
+
+
+def axpy(y, x, s):
+    """aria_axpy (src/aria_ops.h:169): y += s * x (returns the new y)"""
+    from .device import DeviceArray
+    dy = DeviceArray.from_host(_f32(y)); dx = DeviceArray.from_host(_f32(x))
+    try:
+        check(lib().aria_hip_axpy_dev(dy.p, dx.p, s, dy.nbytes // 4, None), "aria_hip_axpy_dev")
+        check(lib().aria_hip_stream_sync(None), "aria_hip_axpy_dev")
+        return dy.to_host()
+    finally:
+        dy.free(); dx.free()
+
+
 def pingpong(x, v, noise, tc, tn):
     y = _f32(x).copy()
     v = _f32(v); noise = _f32(noise)

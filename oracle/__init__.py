@@ -30,10 +30,17 @@ _f = C.c_float
 _sz = C.c_size_t
 
 
+DROPIN = os.path.join(HERE, "_ref", "dropin")
+
+
 def build(ref: bool = True) -> None:
     """Compile the checkers (make -C oracle). The reference part is skipped by the
-    Makefile when the reference tree is absent."""
+    Makefile when the reference tree is absent. With ref, the drop-in link check
+    (the reference's -DARIA_CUDA objects, CLI and tests/test_cuda.c linked against
+    libaria_hip.so) is built too, when the backend library exists."""
     subprocess.run(["make", "-s", "-C", HERE, "-B", "all" if ref else "oracle"], check=True)
+    if ref:
+        subprocess.run(["make", "-s", "-C", HERE, "-B", "-j8", "dropin"], check=True)
 
 
 def _fp(a):
@@ -95,6 +102,24 @@ class _Lib:
         _chk(a, np.float32); _chk(b, np.float32)
         y = np.empty_like(a)
         self._fn("add")(_fp(y), _fp(a), _fp(b), self._n(a.size))
+        return y
+
+    def addto(self, y, a):
+        """y + a as aria_addto does in place (returns the new y)"""
+        y = _chk(y, np.float32).copy(); _chk(a, np.float32)
+        self._fn("addto")(_fp(y), _fp(a), self._n(a.size))
+        return y
+
+    def scale(self, x, s):
+        _chk(x, np.float32)
+        y = np.empty_like(x)
+        self._fn("scale")(_fp(y), _fp(x), _f(s), self._n(x.size))
+        return y
+
+    def axpy(self, y, x, s):
+        """y + s*x as aria_axpy does in place (returns the new y)"""
+        y = _chk(y, np.float32).copy(); _chk(x, np.float32)
+        self._fn("axpy")(_fp(y), _fp(x), _f(s), self._n(x.size))
         return y
 
     def softmax(self, x, mask=None):
@@ -195,6 +220,39 @@ class _Lib:
                                   _fp(mask), None)
         return out
 
+    # ---- sampler (reference only: src/aria_sampler.c) ----
+    def build_schedule(self, steps, sigma_max=1.0, shift=1, seq_len=1296):
+        """aria_build_schedule (src/aria_sampler.c:167-200) with the reference class defaults
+        of the shift type (aria_dist_shift_defaults); shift 1 = LOGSNR. steps + 1 sigmas."""
+        cfg = DistShift()
+        self.lib.aria_dist_shift_defaults(C.byref(cfg), _i(shift))
+        out = np.empty(steps + 1, np.float32)
+        self.lib.aria_build_schedule(_fp(out), _i(steps), _f(sigma_max), C.byref(cfg), _i(seq_len))
+        return out
+
+    def pingpong_cb(self, x, sigmas, velocity, injected_noise):
+        """aria_pingpong_cb (src/aria_sampler.c:203-229) with injected noise [steps, n]:
+        velocity(step, x, t) -> v is called through the reference's denoiser callback
+        (aria_denoiser_fn, src/aria_sampler.h:61). Returns the final x."""
+        x = np.ascontiguousarray(x, np.float32).copy()
+        n = x.size
+        steps = len(sigmas) - 1
+        sig = np.ascontiguousarray(sigmas, np.float32)
+        nz = np.ascontiguousarray(injected_noise, np.float32).reshape(steps, n)
+        calls = [0]
+
+        def cb(ctx, xp, t, vout, nn):
+            xa = np.ctypeslib.as_array(xp, shape=(nn,)).copy()
+            v = np.ascontiguousarray(velocity(calls[0], xa, t), np.float32).reshape(nn)
+            C.memmove(vout, v.ctypes.data, nn * 4)
+            calls[0] += 1
+
+        fn = DENOISE_FN(cb)
+        self.lib.aria_pingpong_cb(_fp(x), _i(n), _fp(sig), _i(steps), fn, None, None, _fp(nz),
+                                  None, None, None, None)
+        assert calls[0] == steps
+        return x
+
     def _n(self, n):
         # the reference's elementwise ops take int n; the port takes size_t
         return _sz(n) if self.p == "or_" else _i(n)
@@ -220,6 +278,18 @@ class _Lib:
                                         _fp(ctx), _i(Sc), _i(dim_ctx), _fp(gcond), _fp(cos_t), _fp(sin_t),
                                         _i(rot), C.byref(w), _i(0))
         return y
+
+
+# aria_denoiser_fn (src/aria_sampler.h:61): void (*)(void *ctx, const float *x, float t, float *v, int n)
+DENOISE_FN = C.CFUNCTYPE(None, C.c_void_p, _F, C.c_float, _F, C.c_int)
+
+
+class DistShift(C.Structure):
+    """aria_dist_shift (src/aria_sampler.h:44-50)"""
+    _fields_ = [("type", C.c_int), ("anchor_length", C.c_float), ("anchor_logsnr", C.c_float),
+                ("rate", C.c_float), ("logsnr_end", C.c_float), ("base_shift", C.c_float),
+                ("max_shift", C.c_float), ("use_sine", C.c_int), ("alpha_min", C.c_float),
+                ("alpha_max", C.c_float), ("min_length", C.c_float), ("max_length", C.c_float)]
 
 
 # aria_dit_block_w, src/aria_sa3_dit.h:40-48 (21 pointers in this order)

@@ -24,7 +24,11 @@
  *                     the dot products, one-hot weights pick one column).
  *   or_linear         vs an independent float64 numpy matmul; KAT tests/test_ops.c:53-63.
  *   or_attention      vs compiled reference aria_attention; uniform-score closed form.
- *   or_pingpong       tc=tn=0 identity; vs numpy float32 step-by-step rounding.
+ *   or_add/addto/scale/axpy  bit-exact vs the compiled reference aria_add/addto/scale/axpy;
+ *                     closed forms (s = 0, s = 1, x + (-x) = 0, exact small integers).
+ *   or_pingpong       bit-exact vs the compiled reference sampler loop aria_pingpong_cb
+ *                     (src/aria_sampler.c:203-229) over 8 LogSNR steps with injected noise;
+ *                     closed forms tn=1 -> noise, tc=1,tn=0 -> x-v, tc=tn=0 identity.
  */
 #include "aria_oracle.h"
 #include <math.h>
@@ -131,6 +135,13 @@ void or_add(float *y, const float *a, const float *b, size_t n) {
 }
 void or_addto(float *y, const float *a, size_t n) {
     for (size_t i = 0; i < n; i++) y[i] += a[i];
+}
+/* src/aria_cpu.c:995-1000: y = x*s and y += s*x (a product, then a sum: no contraction) */
+void or_scale(float *y, const float *x, float s, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] = x[i] * s;
+}
+void or_axpy(float *y, const float *x, float s, size_t n) {
+    for (size_t i = 0; i < n; i++) y[i] += s * x[i];
 }
 
 /* tanh GELU, src/aria_cpu.c:742-749, evaluated left to right as written:

@@ -39,6 +39,8 @@ void or_gate_residual(float *out, const float *res, const float *o, const float 
 /* ---- elementwise ---- */
 void or_add(float *y, const float *a, const float *b, size_t n);
 void or_addto(float *y, const float *a, size_t n);
+void or_scale(float *y, const float *x, float s, size_t n);
+void or_axpy(float *y, const float *x, float s, size_t n);
 void or_gelu_tanh(float *x, size_t n);
 void or_silu(float *x, size_t n);
 void or_silu_gate(float *out, const float *gate, const float *up, size_t n);

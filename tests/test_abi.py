@@ -98,25 +98,88 @@ def test_oracle_is_not_linked_into_product(libpath):
     assert not [s for s in exp if s.startswith("or_")]
 
 
-def test_struct_layouts(tmp_path):
-    """The restated reference types are byte-compatible: sizes and offsets as the reference
-    headers give them on x86-64 (src/aria_sa3_dit.h:40-48, 128-145, src/aria_steer.h:26-38)."""
-    src = tmp_path / "layout.c"
-    src.write_text("""
-#include <stdio.h>
-#include <stddef.h>
-#include "aria_dit.h"
-int main(void) {
-    printf("%zu %zu %zu %zu %zu %zu %zu %zu %zu %zu\\n",
-           sizeof(aria_dit_block_w), sizeof(aria_sa3_dit_view), offsetof(aria_sa3_dit_view, blocks),
-           sizeof(aria_sa3_dit_req_view), offsetof(aria_sa3_dit_req_view, cross_ed),
-           offsetof(aria_sa3_dit_req_view, steer), sizeof(aria_steer), sizeof(aria_steer_set),
-           offsetof(aria_sa3_dit_req_view, has_local), sizeof(aria_dtype));
-    return 0;
+# every field of each restated type (include/aria_dit.h), in declaration order
+LAYOUT_FIELDS = {
+    "aria_dit_block_w": ["pre_norm", "cross_norm", "ff_norm", "sa_to_qkv", "sa_q_norm", "sa_k_norm", "sa_to_out",
+                         "ca_to_q", "ca_to_kv", "ca_q_norm", "ca_k_norm", "ca_to_out", "ff_in_w", "ff_in_b",
+                         "ff_out_w", "ff_out_b", "to_scale_shift_gate", "to_local0_w", "to_local0_b",
+                         "to_local2_w", "to_local2_b"],
+    "aria_sa3_dit_view": ["depth", "ed", "num_heads", "head_dim", "inner", "io_ch", "n_mem", "rot_dim",
+                          "differential", "preprocess", "postprocess", "project_in", "project_out",
+                          "memory_tokens", "blocks"],
+    "aria_sa3_dit_req_view": ["T", "S", "n_cond", "depth", "global_seconds", "rope_cos", "rope_sin", "cross_k",
+                              "cross_v", "cross_kd", "cross_ed", "local_emb", "has_local", "steer"],
+    "aria_steer": ["site", "op", "layer", "dir", "dim", "dir_norm2", "scale", "step_lo", "step_hi"],
+    "aria_steer_set": ["items", "n"],
 }
-""")
-    exe = tmp_path / "layout"
-    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src), "-o",
-                    str(exe)], check=True)
-    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    assert got == [168, 88, 80, 96, 64, 88, 48, 16, 80, 4]
+DTYPE_VALUES = ["ARIA_F32", "ARIA_F16", "ARIA_BF16", "ARIA_Q8", "ARIA_Q4", "ARIA_Q8A8", "ARIA_DTYPE_AUTO"]
+
+
+def _layout_program(include):
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{include}"', "int main(void) {"]
+    for t, fields in LAYOUT_FIELDS.items():
+        lines.append(f'    printf("{t} %zu\\n", sizeof({t}));')
+        for f in fields:
+            lines.append(f'    printf("{t}.{f} %zu %zu\\n", offsetof({t}, {f}), sizeof((({t} *)0)->{f}));')
+    lines.append('    printf("aria_dtype %zu\\n", sizeof(aria_dtype));')
+    for v in DTYPE_VALUES:
+        lines.append(f'    printf("{v} %d\\n", (int){v});')
+    lines += ["    return 0;", "}"]
+    return "\n".join(lines) + "\n"
+
+
+def _layout(tmp_path, tag, include, incdir):
+    src = tmp_path / f"layout_{tag}.c"
+    src.write_text(_layout_program(include))
+    exe = tmp_path / f"layout_{tag}"
+    subprocess.run(["gcc", "-std=c11", "-D_GNU_SOURCE", "-w", "-I", incdir, str(src), "-o", str(exe)], check=True)
+    return subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines()
+
+
+REF_SRC = "/root/reference/src"
+
+
+def test_struct_layouts(tmp_path):
+    """The restated reference types are byte-compatible: every field's offset and size, each
+    type's size and the aria_dtype values, compiled from include/aria_dit.h and from the
+    reference's own headers (src/aria_sa3_dit.h:40-48, 128-145, src/aria_steer.h:26-38,
+    src/aria_quant.h:27-35) by the same program. Where the reference tree is absent (the GPU
+    box) the sizes measured from it are checked instead."""
+    mine = _layout(tmp_path, "mine", "aria_dit.h", os.path.join(ROOT, "include"))
+    if os.path.exists(os.path.join(REF_SRC, "aria_sa3_dit.h")):
+        theirs = _layout(tmp_path, "ref", "aria_sa3_dit.h", REF_SRC)
+        assert mine == theirs, [(a, b) for a, b in zip(mine, theirs) if a != b]
+    got = dict(ln.rsplit(" ", 1) if ln.count(" ") == 1 else (ln, "") for ln in mine)
+    assert [int(got[t]) for t in ("aria_dit_block_w", "aria_sa3_dit_view", "aria_sa3_dit_req_view", "aria_steer",
+                                  "aria_steer_set", "aria_dtype")] == [168, 88, 96, 48, 16, 4]
+
+
+def test_reference_callers_link_against_backend(libpath):
+    """The drop-in: the reference's own library sources and CLI (src/main.c), compiled with
+    -DARIA_CUDA as its `cuda` target does (Makefile:175-191), and its device parity program
+    tests/test_cuda.c link against libaria_hip.so with --no-undefined in place of
+    aria_cuda.o -lcudart -lcublas (oracle/Makefile `dropin`). Every device symbol those
+    callers use is one the backend exports, and test_cuda skips cleanly without a device."""
+    import oracle
+    if os.path.exists(os.path.join(REF_SRC, "aria_model_sa3.c")):
+        subprocess.run(["make", "-s", "-C", os.path.dirname(oracle.__file__), "-j8", "dropin"], check=True)
+    cli = os.path.join(oracle.DROPIN, "aria")
+    tc = os.path.join(oracle.DROPIN, "test_cuda_hip")
+    if not (os.path.exists(cli) and os.path.exists(tc)):
+        pytest.skip("drop-in binaries not built (reference tree absent)")
+    exp = exported_symbols(libpath)
+    for exe in (cli, tc):
+        und = subprocess.run(["nm", "-u", exe], capture_output=True, text=True, check=True).stdout.split()
+        dev = {s for s in und if s.startswith("aria_cuda_")}
+        assert dev and not (dev - exp), sorted(dev - exp)
+        ldd = subprocess.run(["ldd", exe], capture_output=True, text=True).stdout
+        assert "libaria_hip.so" in ldd and "not found" not in ldd, ldd
+    cli_und = set(subprocess.run(["nm", "-u", cli], capture_output=True, text=True).stdout.split())
+    # the DiT/decoder seam of src/aria_model_sa3.c:487-510, 569-601, 634-656
+    assert {"aria_cuda_dit_create", "aria_cuda_dit_set_request", "aria_cuda_dit_step", "aria_cuda_dit_sample",
+            "aria_cuda_dec_create", "aria_cuda_int8_tc", "aria_cuda_recommended"} <= cli_und
+    import aria_amd
+    if aria_amd.lib().aria_cuda_available():
+        pytest.skip("a HIP device is present (tests/test_gpu_dropin.py runs test_cuda there)")
+    out = subprocess.run([tc], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0 and "SKIP" in out.stdout, out.stdout

@@ -368,6 +368,47 @@ def test_dit_packed_overlay(hip, port, R, tmp_path):
     assert L.aria_hip_dit_load_overlay(w8.h, str(q4file).encode()) == -1
     q8file = tmp_path / "q8.aria"
     write_overlay(R, M8, q8file, "q8")
+    # the W8A8 model that loads int8 weights from the file (GLU rows interleaved on load, per-row
+    # scales, the captured step re-made) steps bit-identically to one that packs them on the device
+    w8b = make_dit(M8, 5, 4, rot)
+    T8 = 20
+    S8 = M8["memory_tokens"].shape[0] + T8
+    c8, s8 = R.rope_freqs(S8, rot, 10000.0)
+    _, ced8, _ = inputs(6, 1, M8["project_in"].shape[1], T8, n_cond, 256)
+    x8, _, g8 = inputs(301, 1, M8["project_in"].shape[1], T8, n_cond, 256)
+    for d in (w8, w8b):
+        d.set_request(T8, [ced8[0]], c8, s8)
+    y8 = w8.step(x8, g8)                                   # captures w8's step on its own weights
     assert L.aria_hip_dit_load_overlay(w8.h, str(q8file).encode()) == 0
-    for d in (a, b, w8):
+    z8, zb = w8.step(x8, g8), w8b.step(x8, g8)
+    assert np.array_equal(z8.view(np.uint32), zb.view(np.uint32))
+    assert np.array_equal(z8.view(np.uint32), y8.view(np.uint32))
+    for d in (a, b, w8, w8b):
+        d.free()
+
+
+def test_dit_w8a8_env_knob(hip, R, monkeypatch):
+    """ARIA_W8A8 set turns an ARIA_Q8 model into the W8A8 path at create, as the reference's
+    aria_cuda_dit_create does (src/aria_cuda.cu:1186): its steps are bit-identical to an
+    ARIA_Q8A8 model's and differ from a plain Q8 model's."""
+    M = model(23, ed=256, inner=512)
+    T, n_cond, H, rot = 24, 8, 4, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = R.rope_freqs(S, rot, 10000.0)
+    monkeypatch.delenv("ARIA_W8A8", raising=False)
+    q8 = make_dit(M, 3, H, rot)
+    a8 = make_dit(M, 5, H, rot)
+    monkeypatch.setenv("ARIA_W8A8", "1")
+    env = make_dit(M, 3, H, rot)
+    monkeypatch.delenv("ARIA_W8A8")
+    _, ced, _ = inputs(7, 1, io_ch, T, n_cond, ed)
+    x, _, g = inputs(302, 1, io_ch, T, n_cond, ed)
+    ys = []
+    for d in (q8, a8, env):
+        d.set_request(T, [ced[0]], c, s)
+        ys.append(d.step(x, g))
+    assert np.array_equal(ys[2].view(np.uint32), ys[1].view(np.uint32))
+    assert not np.array_equal(ys[0], ys[1])
+    for d in (q8, a8, env):
         d.free()

@@ -290,3 +290,20 @@ def test_softmax_fully_masked_rows(ops, port):
     got = ops.softmax(s, m)
     assert np.all(np.isfinite(got))
     assert_close(got, port.softmax(s, m), 1e-5, 1e-5, "all-masked")
+
+
+@pytest.mark.parametrize("n", [1, 4099, 1 << 20])
+def test_axpy_scale_addto(ops, port, ref, n):
+    """aria_hip_axpy_dev / aria_hip_scale_dev / aria_hip_add_dev with y aliasing its first input
+    (aria_addto), against the reference's aria_axpy / aria_scale / aria_addto
+    (src/aria_cpu.c:989-1000): bit-exact, ragged sizes included."""
+    r = rng(77 + n)
+    x = randn(r, n); y = randn(r, n)
+    for s_ in (0.7071, -3.25):
+        assert np.array_equal(ops.scale(x, s_).view(np.uint32), port.scale(x, s_).view(np.uint32))
+        assert np.array_equal(ops.axpy(y, x, s_).view(np.uint32), port.axpy(y, x, s_).view(np.uint32))
+    assert np.array_equal(ops.addto(y, x).view(np.uint32), port.addto(y, x).view(np.uint32))
+    if ref is not None:
+        assert np.array_equal(ops.axpy(y, x, -3.25).view(np.uint32), ref.axpy(y, x, -3.25).view(np.uint32))
+        assert np.array_equal(ops.scale(x, 0.7071).view(np.uint32), ref.scale(x, 0.7071).view(np.uint32))
+        assert np.array_equal(ops.addto(y, x).view(np.uint32), ref.addto(y, x).view(np.uint32))

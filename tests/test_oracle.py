@@ -169,6 +169,62 @@ def test_modulate_gate_pingpong_rounding(port):
     assert np.array_equal(port.pingpong(x, v, n, float(tc), float(tn)), want.astype(np.float32))
 
 
+def test_elementwise_axpy_scale_addto(port, ref):
+    """or_add / or_addto / or_scale / or_axpy (src/aria_cpu.c:989-1000): bit for bit against the
+    compiled reference; closed forms s = 0 (scale -> +-0, axpy -> y), s = 1 (x), x + (-x) = 0,
+    and small integers (exact in fp32) for the sums."""
+    r = rng(56)
+    x = randn(r, 5003); y = randn(r, 5003)
+    assert np.array_equal(port.scale(x, 1.0), x)
+    assert np.array_equal(port.scale(x, 0.0), x * np.float32(0))
+    assert np.array_equal(port.axpy(y, x, 0.0), y)
+    assert np.array_equal(port.addto(x, -x), np.zeros_like(x))
+    ia = r.integers(-1000, 1000, 64).astype(np.float32); ib = r.integers(-1000, 1000, 64).astype(np.float32)
+    assert np.array_equal(port.axpy(ia, ib, 3.0), ia + 3 * ib)
+    assert np.array_equal(port.addto(ia, ib), ia + ib)
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    for s_ in (0.7071, -3.25, 1e-20):
+        assert np.array_equal(port.scale(x, s_).view(np.uint32), ref.scale(x, s_).view(np.uint32))
+        assert np.array_equal(port.axpy(y, x, s_).view(np.uint32), ref.axpy(y, x, s_).view(np.uint32))
+    assert np.array_equal(port.addto(y, x).view(np.uint32), ref.addto(y, x).view(np.uint32))
+    assert np.array_equal(port.add(y, x).view(np.uint32), ref.add(y, x).view(np.uint32))
+
+
+def test_pingpong_pinned_to_reference_sampler(port, ref):
+    """or_pingpong against the reference's own sampler loop, aria_pingpong_cb
+    (src/aria_sampler.c:203-229, update at :214-219), run through its denoiser callback with
+    injected noise over several steps of the reference's LogSNR schedule: bit for bit at every
+    step. Closed forms: tn = 1 returns the noise; tc = 1, tn = 0 returns x - v; tc = tn = 0 is
+    the identity. A swapped tc/tn or a sign error fails the first check."""
+    r = rng(55)
+    x = randn(r, 1000); v = randn(r, 1000); n = randn(r, 1000)
+    assert np.array_equal(port.pingpong(x, v, n, 0.0, 0.0), x)
+    assert np.array_equal(port.pingpong(x, v, n, 0.5, 1.0), n)
+    assert np.array_equal(port.pingpong(x, v, n, 1.0, 0.0), (x - v).astype(np.float32))
+    if ref is None:
+        pytest.skip("oracle/_ref not built")
+    steps, size = 8, 4096
+    sig = ref.build_schedule(steps)          # LOGSNR at seq_len 1296, sigma_max 1
+    assert sig[0] == 1.0 and sig[-1] == 0.0 and np.all(np.diff(sig) < 0)
+    x0 = randn(r, size)
+    noise = randn(r, (steps, size))
+    V = randn(r, (steps, size))
+    # a velocity that depends on the step, the current x and t, so a call out of order or a
+    # stale x fails
+    vel = lambda i, xa, t: (V[i] * np.float32(t) + np.float32(0.25) * xa).astype(np.float32)
+    want = ref.pingpong_cb(x0, sig, vel, noise)
+    xs = x0.copy()
+    for i in range(steps):
+        xs = port.pingpong(xs, vel(i, xs, sig[i]), noise[i], float(sig[i]), float(sig[i + 1]))
+    assert np.array_equal(xs.view(np.uint32), want.view(np.uint32))
+    # a planted mistake (tc and tn swapped) is caught by the same comparison
+    xb = x0.copy()
+    for i in range(steps):
+        xb = port.pingpong(xb, vel(i, xb, sig[i]), noise[i], float(sig[i + 1]), float(sig[i]))
+    assert not np.array_equal(xb, want)
+
+
 def test_softmax_invariants(port):
     r = rng(6)
     s = randn(r, (16, 300), 2.0)
