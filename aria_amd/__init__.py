@@ -98,6 +98,7 @@ SIGNATURES = {
     "aria_hip_linear_q8a8_dev": (_i, [_P, _P, _i, _P, _P, _P, _i, _i, _i, _P, _P]),
     "aria_hip_qlinear_ex_dev": (_i, [_P, _i, _P, _i, _i, _P, _P, _P, _i, _i, _i, _i, _P]),
     "aria_hip_linear_q8_dev": (_i, [_P, _P, _P, _P, _P, _i, _i, _i, _P]),
+    "aria_hip_qlinear_noalloc_dev": (_i, [_P, _i, _P, _i, _i, _P, _P, _P, _i, _i, _i, _P]),
     "aria_hip_linear_q4_dev": (_i, [_P, _P, _P, _P, _P, _i, _i, _i, _P]),
     "aria_hip_qkv_prep_dev": (_i, [_P, _i, _i, _i, _i, _i, _P, _P, _P, _P, _P, _i, _f, _P]),
     "aria_hip_flash_attention_dev": (_i, [_P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _P]),

@@ -1,0 +1,93 @@
+/*
+ * k_noalloc.hip - the allocation-free form of the dequant-on-use GEMM entry point.
+ *
+ * aria_hip_qlinear_dev with fp32 activations stages them as fp16 in device memory it
+ * allocates per call (stream-ordered pool) before the MFMA kernel runs. Callers that must
+ * not allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc) call aria_hip_qlinear_noalloc_dev instead: the staging lives in `scratch`,
+ * a file-scope device array of ARIA_HIP_NOALLOC_SCRATCH bytes that each GPU holds for the
+ * life of the process. Its device address is resolved once per device with
+ * hipGetSymbolAddress (host code sees only a stand-in for the array's name) and kept per
+ * device; every kernel argument and copy uses that address.
+ *
+ * Every call on one GPU shares that GPU's array and the array keeps the last call's
+ * contents: calls that overlap on one GPU (two streams, two threads) race on it. The
+ * staging is fully written before the GEMM reads it, so nothing needs clearing.
+ */
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+
+extern "C" {
+#include "aria_hip.h"
+#include "aria_hip_internal.h"
+#include "aria_hip_kernels.h"
+}
+
+#define ARIA_WQ8 0
+#define ARIA_WQ4 1
+#define ARIA_WF16 2
+
+static __device__ __align__(256) unsigned char scratch[ARIA_HIP_NOALLOC_SCRATCH];
+
+#define NOALLOC_MAX_DEV 64
+static std::mutex g_mu;
+static void *g_ptr[NOALLOC_MAX_DEV];   /* device address of `scratch`, per device */
+
+/* the current device's scratch address, resolved on the first call on that device */
+static int scratch_addr(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return aria_hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= NOALLOC_MAX_DEV) {
+        aria_hip_set_error("aria_hip_qlinear_noalloc_dev: device %d beyond the %d the scratch table holds", dev,
+                           NOALLOC_MAX_DEV);
+        return ARIA_HIP_EINVAL;
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return aria_hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                                        "hipGetSymbolAddress (scratch)");
+        g_ptr[dev] = p;
+    }
+    *out = g_ptr[dev];
+    return 0;
+}
+
+extern "C" int aria_hip_qlinear_noalloc_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype,
+                                            const void *dq, const float *dscale, const float *db, int M, int K,
+                                            int N, void *stream) {
+    int rc = aria_hip_ensure();
+    if (rc) return rc;
+    if (M < 0 || K <= 0 || N < 0 || (wtype != ARIA_WQ8 && wtype != ARIA_WQ4 && wtype != ARIA_WF16) ||
+        (M && N && (!dy || !dx || !dq || (wtype != ARIA_WF16 && !dscale)))) {
+        aria_hip_set_error("aria_hip_qlinear_noalloc_dev: invalid argument (M %d, K %d, N %d, wtype %d)", M, K, N,
+                           wtype);
+        return ARIA_HIP_EINVAL;
+    }
+    if (M == 0 || N == 0) return 0;
+    hipStream_t s = aria_hip_stream(stream);
+    const void *xa = dx;
+    int xh = x_f16;
+    if (!x_f16 && K % 32 == 0 && ((uintptr_t)dx & 15u) == 0) {
+        /* the fp16 staging of aria_hip_qlinear_dev, in the static scratch */
+        const size_t need = (size_t)M * K * 2;
+        if (need > ARIA_HIP_NOALLOC_SCRATCH) {
+            aria_hip_set_error("aria_hip_qlinear_noalloc_dev: fp16 staging of %d x %d activations needs %zu bytes, "
+                               "above the %zu-byte scratch; split M or pass fp16 activations",
+                               M, K, need, (size_t)ARIA_HIP_NOALLOC_SCRATCH);
+            return ARIA_HIP_EINVAL;
+        }
+        void *p = nullptr;
+        if ((rc = scratch_addr(&p))) return rc;
+        hipError_t e = aria_k_f32_to_f16((uint16_t *)p, (const float *)dx, (size_t)M * K, s);
+        if (e != hipSuccess) return aria_hip_fail(e, "k_f32_to_f16 (scratch staging)");
+        xa = p;
+        xh = 1;
+    }
+    hipError_t e = aria_k_qgemm_t(dy, y_f16, xa, xh, wtype, dq, dscale, db, M, K, N, 0, 0, s);
+    if (e != hipSuccess) return aria_hip_fail(e, "k_qgemm (no-alloc)");
+    return 0;
+}

@@ -146,6 +146,17 @@ int aria_hip_qlinear_ex_dev(void *dy, int y_f16, const void *dx, int x_f16, int 
                             void *stream);
 int aria_hip_linear_q8_dev(float *dy, const float *dx, const int8_t *dq, const float *dscale,
                            const float *db, int M, int K, int N, void *stream);
+/* aria_hip_qlinear_dev that allocates nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments and results, bit for bit; the
+ * fp16 staging of fp32 activations goes to a static device array of
+ * ARIA_HIP_NOALLOC_SCRATCH bytes per GPU instead of per-call pool memory, so M * K * 2 must
+ * not exceed it (ARIA_HIP_EINVAL otherwise; fp16 activations need no staging). Every call
+ * on one GPU shares that array: calls that overlap on one GPU (other streams or threads)
+ * race and must be serialised by the caller. */
+#define ARIA_HIP_NOALLOC_SCRATCH ((size_t)32 << 20)
+int aria_hip_qlinear_noalloc_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
+                                 const float *dscale, const float *db, int M, int K, int N, void *stream);
 int aria_hip_linear_q4_dev(float *dy, const float *dx, const uint8_t *dq, const float *dscale,
                            const float *db, int M, int K, int N, void *stream);
 
