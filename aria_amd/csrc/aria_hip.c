@@ -451,7 +451,7 @@ int aria_hip_q4_dequant_dev(float *dW, const uint8_t *dq, const float *dscale, i
 int aria_hip_qlinear_ex_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
                             const float *dscale, const float *db, int M, int K, int N, int tiles, void *stream) {
     ENSURE();
-    REQ(M >= 0 && K > 0 && N >= 0 && tiles >= 0 && tiles <= 12);
+    REQ(M >= 0 && K > 0 && N >= 0 && tiles >= 0 && tiles <= 32);
     REQ(wtype == ARIA_WQ8 || wtype == ARIA_WQ4 || wtype == ARIA_WF16);
     REQ(M == 0 || N == 0 || (dy && dx && dq && (wtype == ARIA_WF16 || dscale)));
     if (M == 0 || N == 0) return 0;

@@ -400,6 +400,18 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
         return hipGetLastError();
     } else {
     if constexpr (WT != ARIA_WF16) {
+        /* the LDS-DMA kernel (k_qgemm_big.hip): explicit tiles 13.. (configuration tiles - 13),
+         * or picked for the shapes where it measured fastest: N <= 1024 without HEADS (96 x 128
+         * tiles, two workgroups per CU), the N = 3072 qkv projection with HEADS (128 x 256), other
+         * N <= 3072 without HEADS (128 x 128, two per CU) */
+        if (tiles >= 13) return qgemm_big_launch(a, WT, tiles - 13, s);
+        if (tiles == 0 && a.K % 64 == 0 && (WT != ARIA_WQ4 || ((uintptr_t)a.scale & 15u) == 0) &&
+            (!a.gelu || a.epi.mode == ARIA_EPI_STORE)) {
+            const bool heads = a.epi.mode == ARIA_EPI_HEADS;
+            const int cfg = (!heads && a.N <= 1024) ? 0 : (heads && a.N > 1024 && a.N <= 3072) ? 1
+                          : (!heads && a.N <= 3072) ? 2 : -1;
+            if (cfg >= 0) return qgemm_big_launch(a, WT, cfg, s);
+        }
         /* weights-in-registers kernel: explicit tiles 9..12 (BM = 32 * (tiles - 8)), or the pick */
         int fm = (tiles > NCFG) ? tiles - NCFG : (tiles == 0 ? pick_wr(a.M, a.N, a.K) : 0);
         /* Q8 with N and K <= 1024 (the DiT's sa_out / ca_out): 64 x 64 LDS-operand tiles, 2.5

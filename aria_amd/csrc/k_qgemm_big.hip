@@ -1,0 +1,371 @@
+/*
+ * k_qgemm_big.hip - the large-tile dequant-on-use GEMM (gfx950 MFMA):
+ * y[M,N] = x[M,K] W[N,K]^T (+ b) for Q8 / Q4 weights and fp16 activations, K % 64 == 0.
+ * Replaces the same reference functions as k_qgemm.hip (aria_linear_q8 / aria_linear_q4,
+ * src/aria_quant.c:98-145, 469-538; the reference's device form dequantizes into an fp16
+ * scratch and calls cublasGemmEx, src/aria_cuda.cu:1009-1035). Shares the argument block,
+ * the unpack and the fused epilogue with the other GEMM kernels (qgemm_dev.h).
+ *
+ * Workgroup: 4 waves share one activation tile of BM = 32 FM rows; wave w owns FN blocks
+ * of 32 weight rows (BN = 128 FN per workgroup) and loads them straight from the packed
+ * layout into registers in the MFMA operand layout. The cost that grows with the tile is
+ * the unpack: each weight is unpacked once per workgroup and feeds BM rows, so unpack VALU
+ * per MFMA falls as 1 / FM; the LDS bytes per MFMA fall as 1 / FN (FN = 2: 0.5 KB per
+ * 32x32x16 MFMA, half the LDS rate at full MFMA rate). FM up to 8 keeps 32 FM FN
+ * accumulator registers per lane (the AGPRs) and one wave per SIMD.
+ *
+ * Pipeline, K-tile 64, three stages: the activation tile of K-tile t arrives in LDS by
+ * LDS DMA (global_load_lds_dwordx4, no staging registers) two K-tiles before it is
+ * multiplied, into LDS buffer t % 3; the weights of K-tile t arrive in register stage
+ * t % 3, also two K-tiles ahead. Step t: issue the loads of t + 2, multiply t, wait for
+ * the loads of t + 1 (issued one whole step earlier), one barrier. The three buffers are
+ * separate LDS objects picked by compile-time indices, so the compiler can see that the
+ * fragment reads of buffer t never touch the pending DMA of buffers t + 1, t + 2.
+ *
+ * Contraction order inside a K-tile (as in k_qgemm_wr.hip): lane half h = l / 32 covers
+ * k in [32h, 32h + 32) and MFMA step ks its 8 k at 32h + 8ks, for both operands; a Q4
+ * lane's range is exactly one quantization block (one [min, step] pair per K-tile). So the
+ * accumulation order over k, and with it every output bit, equals k_qgemm_wr's.
+ */
+#include "qgemm_dev.h"
+
+namespace {
+
+constexpr int KB = 64;   /* K-tile */
+
+/* activation tile [BM][64] halves: 8 chunks of 16 B per row, logical chunk c of row r at
+ * c ^ ((r >> 1) & 7) (conflict-free fragment reads: 32 rows x one chunk per lane half) */
+__device__ __forceinline__ int xo(int r, int c) { return r * KB + ((c ^ ((r >> 1) & 7)) << 3); }
+
+template <int WT, int FN>
+struct WSt {              /* one lane's raw weights of one K-tile, FN 32-row blocks */
+    static constexpr int NW = (WT == ARIA_WQ8) ? 8 : 6;   /* Q8: 32 B; Q4: 16 B nibbles + [min, step] */
+    uint32_t w[FN][NW];
+};
+
+__device__ __forceinline__ uint32_t and_or_v(uint32_t w, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(magic));
+    return r;
+}
+
+/* the per-block offsets of the Q4 unpack: (1024 + n) * step + (min - 1024 step) = min + n step
+ * for a low nibble, (1024 + 16 n) * step / 16 + (min - 64 step) for a high one */
+struct QOff { float a, b, st, s16; };
+template <int WT, int FN>
+__device__ __forceinline__ QOff qoff(const WSt<WT, FN> &s, int j) {
+    QOff o;
+    if constexpr (WT == ARIA_WQ4) {
+        const float mn = __builtin_bit_cast(float, s.w[j][4]);
+        o.st = __builtin_bit_cast(float, s.w[j][5]);
+        o.s16 = o.st * 0.0625f;
+        o.a = __builtin_fmaf(-1024.0f, o.st, mn);
+        o.b = __builtin_fmaf(-64.0f, o.st, mn);
+    } else {
+        o.a = o.b = o.st = o.s16 = 0.0f;
+    }
+    return o;
+}
+
+/* the 8 fp16 weights of block j for MFMA step ks (see k_qgemm_wr.hip for the arithmetic:
+ * the value the reference dequantizes, rounded to fp16) */
+template <int WT, int FN>
+__device__ __forceinline__ half8_t wfrag(const WSt<WT, FN> &s, int j, int ks, uint32_t magic, const QOff &f) {
+    uint32_t o[4];
+    if constexpr (WT == ARIA_WQ4) {
+        const uint32_t w = s.w[j][ks], u = w >> 8;
+        const half2_t t0 = __builtin_bit_cast(half2_t, and_or_v(w, 0x000F000Fu, magic));
+        const half2_t t1 = __builtin_bit_cast(half2_t, and_or_v(w, 0x00F000F0u, magic));
+        const half2_t t2 = __builtin_bit_cast(half2_t, and_or_v(u, 0x000F000Fu, magic));
+        const half2_t t3 = __builtin_bit_cast(half2_t, and_or_v(u, 0x00F000F0u, magic));
+        const half2_t h0 = {(_Float16)__builtin_fmaf((float)t0[0], f.st, f.a), (_Float16)__builtin_fmaf((float)t1[0], f.s16, f.b)};
+        const half2_t h1 = {(_Float16)__builtin_fmaf((float)t2[0], f.st, f.a), (_Float16)__builtin_fmaf((float)t3[0], f.s16, f.b)};
+        const half2_t h2 = {(_Float16)__builtin_fmaf((float)t0[1], f.st, f.a), (_Float16)__builtin_fmaf((float)t1[1], f.s16, f.b)};
+        const half2_t h3 = {(_Float16)__builtin_fmaf((float)t2[1], f.st, f.a), (_Float16)__builtin_fmaf((float)t3[1], f.s16, f.b)};
+        o[0] = __builtin_bit_cast(uint32_t, h0); o[1] = __builtin_bit_cast(uint32_t, h1);
+        o[2] = __builtin_bit_cast(uint32_t, h2); o[3] = __builtin_bit_cast(uint32_t, h3);
+    } else {
+        q8x4_to_h(s.w[j][2 * ks], o[0], o[1]);
+        q8x4_to_h(s.w[j][2 * ks + 1], o[2], o[3]);
+    }
+    return __builtin_bit_cast(half8_t, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+/* s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding) */
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+/* One LDS DMA instruction: every lane moves 16 B from global address g to LDS byte address
+ * m0 + 16 * lane (m0 wave-uniform). Issued as inline assembly, so the compiler neither waits
+ * for it nor reorders memory accesses across it: the kernel waits on vmcnt itself. */
+__device__ __forceinline__ void dma16(const void *g, uint32_t m0) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(m0);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m), "v"(g) : "memory");
+}
+
+/* Layout of one pipeline stage in LDS (bytes):
+ *   [0, 128 BM)            activations [BM][64] fp16, chunk-swizzled (xo)
+ *   Q8: [.., + 64 BN)      weights [BN][64] int8; 16 B chunk c of row r at c ^ ((r >> 2) & 3)
+ *   Q4: [.., + 32 BN)      nibbles [BN][32 B]
+ *       [.., + 4096)       [min, step] pairs of the K-tile, 16 B per row: wave w's 64 slots
+ *                          at 1024 w (FN = 1: rows 32w.. in slots 0-31, 32-63 repeat them) */
+template <int WT, int FM, int FN>
+struct Stage {
+    static constexpr int BM = 32 * FM, BN = 128 * FN;
+    static constexpr int A = BM * 128;
+    static constexpr int WQ = WT == ARIA_WQ8 ? BN * 64 : BN * 32;
+    static constexpr int WS = WT == ARIA_WQ8 ? 0 : 4096;
+    static constexpr int BYTES = A + WQ + WS;
+    /* VMEM instructions one wave issues per K-tile */
+    static constexpr int DMA = FM + (WT == ARIA_WQ8 ? 2 * FN : FN + 1);
+};
+
+}  // namespace
+
+/* One tile per workgroup; MINB workgroups per CU (MINB = 2 when the tile's registers and
+ * LDS allow two: the second workgroup's waves cover one workgroup's barrier waits and its
+ * epilogue). The tiles of an XCD are a contiguous run in M-major order (xcd_tile). */
+template <int WT, int FM, int FN, int MODE, bool GELU, int MINB, int NS, int NST>
+__global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T) {
+    using St = Stage<WT, FM, FN>;   /* one 64-deep sub-tile; a pipeline stage holds NS of them */
+    constexpr int SB = NS * St::BYTES;                                 /* stage bytes */
+    constexpr int PD = NST - 1;                                        /* prefetch distance */
+    static_assert(NST >= 2 && NST <= 4, "two to four stages");
+    constexpr int BM = St::BM, BN = St::BN;
+    constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
+    constexpr int EPI_WAVE = 32 * EPI_STRIDE;                          /* bytes per wave */
+    static_assert(NST * SB >= 4 * EPI_WAVE, "the epilogue staging fits the stages");
+    static_assert(NST * SB <= (MINB == 1 ? 160 : 80) * 1024, "the stages fit the LDS");
+    __shared__ __attribute__((aligned(16))) uint8_t smem[NST * SB];
+
+    const int t = xcd_tile(blockIdx.x, T);
+    if (t >= T) return;                     /* uniform per workgroup, before any barrier */
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lrow = lane & 31, lh = lane >> 5;
+    const int KT = a.K / (KB * NS);         /* pipeline steps */
+    uint32_t magic = 0x64006400u;           /* fp16 1024 in both halves, kept in a VGPR */
+    asm volatile("" : "+v"(magic));
+    const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+    constexpr int NWQ = WT == ARIA_WQ8 ? 2 * FN : FN;   /* weight DMA instructions per wave */
+    const int rbase = wave * 32 * FN;                    /* this wave's first weight row */
+
+    /* per-lane global sources of this wave's DMA slots for K-tile 0 of tile (m0, n0);
+     * K-tile kt adds kt * its step */
+    const uint16_t *xsrc[FM];
+    const uint8_t *wsrc[NWQ];
+    const float *ssrc = nullptr;
+    auto sources = [&](int m0, int n0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int p = 256 * i + 64 * wave + lane, r = p >> 3, cp = p & 7;
+            const int c = cp ^ ((r >> 1) & 7);
+            xsrc[i] = (const uint16_t *)a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 8 * c;
+        }
+#pragma unroll
+        for (int i = 0; i < NWQ; i++) {
+            const int p = 64 * i + lane;
+            if constexpr (WT == ARIA_WQ8) {
+                const int r = rbase + (p >> 2), c = (p & 3) ^ ((r >> 2) & 3);
+                wsrc[i] = (const uint8_t *)a.q + (size_t)min(n0 + r, a.N - 1) * a.K + 16 * c;
+            } else {
+                const int r = rbase + (p >> 1);
+                wsrc[i] = (const uint8_t *)a.q + (size_t)min(n0 + r, a.N - 1) * (a.K >> 1) + 16 * (p & 1);
+            }
+        }
+        if constexpr (WT == ARIA_WQ4) {
+            const int r = rbase + (lane & (32 * FN - 1));
+            ssrc = a.scale + (size_t)min(n0 + r, a.N - 1) * a.nblk * 2;
+        }
+    };
+    /* all VMEM of step kt (sub-tiles NS kt .. NS kt + NS - 1) into stage B */
+    auto issue = [&](int B, int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NS; u++) {
+            const int k64 = NS * kt + u;
+            const uint32_t st = sbase + B * SB + u * St::BYTES;
+#pragma unroll
+            for (int i = 0; i < FM; i++) dma16(xsrc[i] + k64 * KB, st + (256 * i + 64 * wave) * 16);
+            if constexpr (WT == ARIA_WQ8) {
+#pragma unroll
+                for (int i = 0; i < NWQ; i++) dma16(wsrc[i] + k64 * KB, st + St::A + rbase * 64 + 1024 * i);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NWQ; i++) dma16(wsrc[i] + k64 * 32, st + St::A + rbase * 32 + 1024 * i);
+                dma16(ssrc + 4 * k64, st + St::A + St::WQ + 1024 * wave);
+            }
+        }
+    };
+    constexpr int DMA = NS * St::DMA;        /* VMEM instructions of one step */
+
+    f32x16_t acc[FM][FN];
+
+    /* one K-tile from stage B: this lane's raw weights from LDS, then 4 MFMA steps of FM x FN
+     * MFMAs; step ks + 1's activation fragments are requested and its weights unpacked while
+     * step ks's MFMAs run */
+    auto compute = [&](auto BB) __attribute__((always_inline)) {
+        constexpr int B = decltype(BB)::value;
+        static_for<NS>([&](auto UU) __attribute__((always_inline)) {
+        const uint8_t *S = smem + B * SB + decltype(UU)::value * St::BYTES;
+        const uint16_t *X = reinterpret_cast<const uint16_t *>(S);
+        WSt<WT, FN> ws;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int r = rbase + 32 * j + lrow;
+            if constexpr (WT == ARIA_WQ8) {
+                const uint8_t *row = S + St::A + r * 64;
+                const uint4 u0 = *reinterpret_cast<const uint4 *>(row + 16 * ((2 * lh) ^ ((r >> 2) & 3)));
+                const uint4 u1 = *reinterpret_cast<const uint4 *>(row + 16 * ((2 * lh + 1) ^ ((r >> 2) & 3)));
+                ws.w[j][0] = u0.x; ws.w[j][1] = u0.y; ws.w[j][2] = u0.z; ws.w[j][3] = u0.w;
+                ws.w[j][4] = u1.x; ws.w[j][5] = u1.y; ws.w[j][6] = u1.z; ws.w[j][7] = u1.w;
+            } else {
+                const uint4 u = *reinterpret_cast<const uint4 *>(S + St::A + r * 32 + 16 * lh);
+                const int slot = FN == 2 ? (32 * j + lrow) : lrow;
+                const uint2 pr = *reinterpret_cast<const uint2 *>(S + St::A + St::WQ + 1024 * wave + 16 * slot + 8 * lh);
+                ws.w[j][0] = u.x; ws.w[j][1] = u.y; ws.w[j][2] = u.z; ws.w[j][3] = u.w;
+                ws.w[j][4] = pr.x; ws.w[j][5] = pr.y;
+            }
+        }
+        QOff f[FN];
+#pragma unroll
+        for (int j = 0; j < FN; j++) f[j] = qoff<WT, FN>(ws, j);
+        half8_t xa[FM], xn[FM], wa[FN], wn[FN];
+#pragma unroll
+        for (int i = 0; i < FM; i++) xa[i] = *reinterpret_cast<const half8_t *>(&X[xo(i * 32 + lrow, 4 * lh)]);
+#pragma unroll
+        for (int j = 0; j < FN; j++) wa[j] = wfrag<WT, FN>(ws, j, 0, magic, f[j]);
+        static_for<4>([&](auto KS) __attribute__((always_inline)) {
+            constexpr int ks = decltype(KS)::value;
+            if constexpr (ks < 3) {
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+                    xn[i] = *reinterpret_cast<const half8_t *>(&X[xo(i * 32 + lrow, 4 * lh + ks + 1)]);
+#pragma unroll
+                for (int j = 0; j < FN; j++) wn[j] = wfrag<WT, FN>(ws, j, ks + 1, magic, f[j]);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[j], xa[i], acc[i][j], 0, 0, 0);
+            if constexpr (ks < 3) {
+#pragma unroll
+                for (int i = 0; i < FM; i++) xa[i] = xn[i];
+#pragma unroll
+                for (int j = 0; j < FN; j++) wa[j] = wn[j];
+            }
+        });
+        });
+    };
+
+    /* workgroup barrier without a memory fence: the loop's only LDS writes are the DMA
+     * transfers, whose completion each wave has waited for on vmcnt just before */
+    auto barrier = []() __attribute__((always_inline)) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    /* step kt (kt % NST == P): step kt + PD requested into stage (P + PD) % NST, step kt
+     * multiplied from stage P, then this wave's transfers of step kt + 1 waited for (those of
+     * later steps stay in flight) and the barrier publishes stage (P + 1) % NST */
+    auto step = [&](auto PP, int kt) __attribute__((always_inline)) {
+        constexpr int P = decltype(PP)::value;
+        const bool more = kt + PD < KT;
+        if (more) issue((P + PD) % NST, kt + PD);
+        compute(IC<P>{});
+        if constexpr (PD >= 2) {
+            if (more) wait_vm<(PD - 1) * DMA>();
+            else wait_vm<0>();
+        } else {
+            wait_vm<0>();
+        }
+        barrier();
+    };
+
+    const int m0 = (t / NTN) * BM, n0 = (t % NTN) * BN;
+    sources(m0, n0);
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    /* prologue: steps 0 .. PD - 1 in flight, then wait for step 0 */
+    static_for<PD>([&](auto PP) __attribute__((always_inline)) {
+        if (decltype(PP)::value < KT) issue(decltype(PP)::value, decltype(PP)::value);
+    });
+    if (KT >= PD) wait_vm<(PD - 1) * DMA>();
+    else wait_vm<0>();
+    barrier();
+    int kt = 0;
+    for (; kt + NST <= KT; kt += NST)
+        static_for<NST>([&](auto PP) __attribute__((always_inline)) { step(PP, kt + decltype(PP)::value); });
+    static_for<NST - 1>([&](auto PP) __attribute__((always_inline)) {
+        if (kt + decltype(PP)::value < KT) step(PP, kt + decltype(PP)::value);
+    });
+    /* every wave is past its last fragment read (the last step's barrier): the stages hold the
+     * epilogue staging */
+    float *E = reinterpret_cast<float *>(smem + wave * EPI_WAVE);
+    epilogue<FM, FN, WT, MODE, GELU>(a, acc, E, lane, m0, n0 + wave * 32 * FN);
+}
+
+template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int NS = 1, int NST = 3>
+static void launch_big_m(const QArgs &a, hipStream_t s) {
+    constexpr int BM = 32 * FM, BN = 128 * FN;
+    const int MT = (a.M + BM - 1) / BM, NTN = (a.N + BN - 1) / BN, T = MT * NTN;
+    const int grid = ((T + 7) / 8) * 8;
+    hipLaunchKernelGGL((k_qgemm_big<WT, FM, FN, MODE, GELU, MINB, NS, NST>), dim3(grid), dim3(256), 0, s, a, NTN, T);
+}
+
+/* one kernel per fused epilogue mode (a run-time mode switch inside the store loop makes
+ * every store wait for the loads of the modes that read); HEADS needs FN = 2 (a head's 64
+ * columns in one wave) */
+template <int WT, int FM, int FN, int MINB>
+static void launch_big(const QArgs &a, hipStream_t s) {
+    switch (a.epi.mode) {
+        case ARIA_EPI_GATE_RES: launch_big_m<WT, FM, FN, ARIA_EPI_GATE_RES, false, MINB>(a, s); break;
+        case ARIA_EPI_ADD: launch_big_m<WT, FM, FN, ARIA_EPI_ADD, false, MINB>(a, s); break;
+        case ARIA_EPI_HEADS:
+            if constexpr (FN >= 2) launch_big_m<WT, FM, FN, ARIA_EPI_HEADS, false, MINB>(a, s);
+            break;
+        case ARIA_EPI_GLU: launch_big_m<WT, FM, FN, ARIA_EPI_GLU, false, MINB>(a, s); break;
+        default:
+            if (a.gelu) launch_big_m<WT, FM, FN, ARIA_EPI_STORE, true, MINB>(a, s);
+            else launch_big_m<WT, FM, FN, ARIA_EPI_STORE, false, MINB>(a, s);
+            break;
+    }
+}
+
+/* the configurations compiled (FM, FN, workgroups per CU), index = the cfg argument; measured
+ * at M = 2592 (DiT shapes), fp16 activations:
+ *   0: 96 x 128, two per CU: N <= 1024 (sa_out, ca_out, ff_out; K = 1024 and 4096)
+ *   1: 128 x 256, one per CU: the qkv projection (HEADS, N = 3072)
+ *   2: 128 x 128, two per CU: N = 3072 without HEADS */
+#define BIG_CFGS(X) X(0, 3, 1, 2) X(1, 4, 2, 1) X(2, 4, 1, 2)
+static const int big_fm[] = {3, 4, 4};
+static const int big_fn[] = {1, 2, 1};
+
+int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
+int qgemm_big_bm(int cfg) { return 32 * big_fm[cfg]; }
+int qgemm_big_bn(int cfg) { return 128 * big_fn[cfg]; }
+
+hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
+    if (a.K % KB || cfg < 0 || cfg >= qgemm_big_ncfg() || (a.gelu && a.epi.mode != ARIA_EPI_STORE) ||
+        (a.epi.mode == ARIA_EPI_HEADS && big_fn[cfg] < 2))
+        return hipErrorInvalidValue;
+#define BIG_CASE(i, fm, fn, mb)                                          \
+    case i:                                                              \
+        if (wt == ARIA_WQ8) launch_big<ARIA_WQ8, fm, fn, mb>(a, s);      \
+        else launch_big<ARIA_WQ4, fm, fn, mb>(a, s);                     \
+        break;
+    if (wt != ARIA_WQ8 && wt != ARIA_WQ4) return hipErrorInvalidValue;
+    switch (cfg) {
+        BIG_CFGS(BIG_CASE)
+        default: return hipErrorInvalidValue;
+    }
+#undef BIG_CASE
+    return hipGetLastError();
+}

@@ -324,5 +324,12 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
 /* the weights-in-registers kernel's launcher (k_qgemm_wr.hip): BM = 32 * fm rows by
  * 256 weight rows per workgroup; wt is ARIA_WQ8 or ARIA_WQ4, activations fp16, K % 64 == 0 */
 hipError_t qgemm_wr_launch(const QArgs &a, int wt, int fm, hipStream_t s);
+/* the large-tile kernel's launcher (k_qgemm_big.hip): configuration cfg of
+ * qgemm_big_ncfg(), BM = qgemm_big_bm(cfg) rows by qgemm_big_bn(cfg) weight rows per
+ * workgroup; Q8 / Q4 weights, fp16 activations, K % 64 == 0 */
+hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s);
+int qgemm_big_ncfg();
+int qgemm_big_bm(int cfg);
+int qgemm_big_bn(int cfg);
 
 #endif /* ARIA_QGEMM_DEV_H */
