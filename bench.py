@@ -71,11 +71,52 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(x, sc, sh, w, q, k, cos64, sin64, scores):
-    """The reference's CPU path (oracle/_ref, compiled from its src/aria_cpu.c) on the same
-    C2 step: reference ops where the reference has them, the restatement for LayerNorm and
-    the modulate glue (static in the reference). Bounded: softmax on 1/8 of the rows,
-    scaled; the rest at full size. Returns the cpu_baseline object or None."""
+def _physical_cores():
+    """distinct (physical id, core id) pairs of /proc/cpuinfo (the reference's physical_cores,
+    src/aria.c); os.cpu_count() when the file lacks them"""
+    pairs, phys = set(), "0"
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("physical id"):
+                phys = ln.split(":", 1)[1].strip()
+            elif ln.startswith("core id"):
+                pairs.add((phys, ln.split(":", 1)[1].strip()))
+    except OSError:
+        pass
+    return len(pairs) or os.cpu_count() or 1
+
+
+def _cpu_threads():
+    """The reference CLI's OpenMP policy, applied before the compiled reference loads:
+    OMP_WAIT_POLICY=active unless set (src/main.c:582), and one thread per physical core
+    unless OMP_NUM_THREADS is set, which wins (src/aria.c:159-167). Returns the team size."""
+    os.environ.setdefault("OMP_WAIT_POLICY", "active")
+    if not os.environ.get("OMP_NUM_THREADS"):
+        os.environ["OMP_NUM_THREADS"] = str(_physical_cores())
+    return int(os.environ["OMP_NUM_THREADS"])
+
+
+def _warm_min(fn, reps):
+    """one untimed call, then the minimum of `reps` timed calls (the reference's --bench warm-min)"""
+    fn()
+    best = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        best = dt if best is None else min(best, dt)
+    return best
+
+
+def cpu_baseline(x, sc, sh, w, q, k, cos64, sin64, scores, rng):
+    """The reference's CPU path (oracle/_ref, compiled from its src/aria_cpu.c, aria_quant.c)
+    on the host cores, with the reference CLI's thread policy. `value` is the same C2 step as
+    the GPU's: reference ops where the reference has them, the restatement for LayerNorm and
+    the modulate glue (static in the reference). Bounded: softmax on 1/8 of the score rows,
+    scaled. The `legs` hold the other configs (C1 chain and softmax; C3 q8 / q4 GEMMs, the q4
+    ones on a quarter of the rows, scaled; C4 one sequence of the q4 block, scaled to the
+    batch of 2). Returns the cpu_baseline object or None."""
+    threads = _cpu_threads()
     import oracle
     R = oracle.ref()
     kind = "reference"
@@ -88,16 +129,18 @@ def cpu_baseline(x, sc, sh, w, q, k, cos64, sin64, scores):
     sub = rows[: rows.shape[0] // 8].copy()
     gamma = np.ones(D, np.float32); beta = np.zeros(D, np.float32)
 
+    def chain(xx, ss, hh):
+        out = np.empty_like(xx)
+        for b in range(xx.shape[0]):
+            hb = P.layernorm(xx[b], gamma, beta, 1e-6)
+            hb = P.adaln_modulate(hb, ss[b], hh[b])
+            hb = R.gelu_tanh(hb)
+            out[b] = R.add(hb, xx[b])
+        return out
+
     def step():
         t = {}
-        t0 = time.perf_counter()
-        out = np.empty_like(x)
-        for b in range(B):
-            hb = P.layernorm(x[b], gamma, beta, 1e-6)
-            hb = P.adaln_modulate(hb, sc[b], sh[b])
-            hb = R.gelu_tanh(hb)
-            out[b] = R.add(hb, x[b])
-        t["chain"] = time.perf_counter() - t0
+        t0 = time.perf_counter(); chain(x, sc, sh); t["chain"] = time.perf_counter() - t0
         t0 = time.perf_counter(); R.rmsnorm(x, w, 1e-6); t["rms"] = time.perf_counter() - t0
         t0 = time.perf_counter(); P.layernorm(x, None, None, 1e-6); t["ln"] = time.perf_counter() - t0
         t0 = time.perf_counter()
@@ -116,18 +159,65 @@ def cpu_baseline(x, sc, sh, w, q, k, cos64, sin64, scores):
         reps += 1
         best = t if best is None else {kk: min(best[kk], t[kk]) for kk in t}
     total = sum(best.values())
-    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    legs = {}
+
+    # C1: the chain on x [2, 216, 1024] and softmax over [2, 16, 216, 216]
+    S1 = 216
+    x1 = rng.standard_normal((B, S1, D), dtype=np.float32)
+    s1 = (2.0 * rng.standard_normal((B * H * S1, S1))).astype(np.float32)
+    tc = _warm_min(lambda: chain(x1, sc, sh), 5)
+    ts = _warm_min(lambda: R.softmax(s1), 5)
+    b_chain, b_sm = 2 * x1.nbytes, 2 * s1.nbytes
+    legs["c1"] = {"chain_us": round(tc * 1e6, 1), "chain_GB/s": round(b_chain / tc / 1e9, 2),
+                  "softmax_us": round(ts * 1e6, 1), "softmax_GB/s": round(b_sm / ts / 1e9, 2),
+                  "sample": "full size, warm-min of 5"}
+
+    # C3: aria_linear_q8 / aria_linear_q4 at M = 2592 (weights ~N(0, 0.02) packed by the reference)
+    c3 = {}
+    for K, N in ((1024, 4096), (4096, 1024)):
+        Wf = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+        X = rng.standard_normal((B * S, K), dtype=np.float32)
+        q8, s8 = R.q8_quant(Wf)
+        q4, s4 = R.q4_quant(Wf)
+        flop = 2.0 * B * S * K * N
+        t8 = _warm_min(lambda: R.linear_q8(X, q8, s8), 3)
+        Xq = np.ascontiguousarray(X[: B * S // 4])
+        t4 = _warm_min(lambda: R.linear_q4(Xq, q4, s4), 1) * 4.0
+        c3[f"q8_K{K}_N{N}"] = {"ms": round(t8 * 1e3, 2), "GFLOP/s": round(flop / t8 / 1e9, 1)}
+        c3[f"q4_K{K}_N{N}"] = {"ms": round(t4 * 1e3, 2), "GFLOP/s": round(flop / t4 / 1e9, 1)}
+    c3["sample"] = "M = 2592 rows: q8 full size, warm-min of 3; q4 on the first 648 rows, one warm + one timed call, x4"
+    legs["c3"] = c3
+
+    # C4: one q4 DiT block (tanh-GELU 4x FFN) on one of the two sequences, the composition of
+    # reference ops (oracle/dit_block.py, pinned to aria_dit_block_forward), x2 for the batch
+    from oracle import dit_block as DB
+    from aria_amd.dit import random_block_weights
+    Wb = random_block_weights(rng, D, 4096, 768, ffn=DB.FFN_GELU)
+    packed = DB.pack_weights(R, Wb, "q4")
+    ctx = rng.standard_normal((256, 768), dtype=np.float32)
+    kc, vc = DB.cross_kv(R, ctx, Wb, H)
+    xb = rng.standard_normal((S, D), dtype=np.float32)
+    gb = (0.1 * rng.standard_normal(6 * D)).astype(np.float32)
+    inv = 1.0 / (10000.0 ** (np.arange(16) * 2.0 / 32))
+    ang = np.arange(S)[:, None] * inv[None, :]
+    c32, s32 = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    tb = _warm_min(lambda: DB.block_forward(R, P, xb, kc, vc, gb, Wb, packed, c32, s32, 32, H, DB.FFN_GELU), 1)
+    legs["c4"] = {"block_us": round(tb * 2 * 1e6, 0), "per_sequence_ms": round(tb * 1e3, 1),
+                  "sample": "one sequence of T = 1296 (the reference block is batch 1), one warm + one timed "
+                            "forward, x2 for the CFG pair; the per-request cross K/V projection excluded, as on the GPU"}
     return {
         "value": round(sum(ab.values()) / total / 1e9, 2),
         "unit": "GB/s",
-        "cores": cores,
+        "cores": threads,
         "kind": kind,
-        "sample": ("one C2 step, warm-min of %d reps on the host CPU (%s): reference aria_rmsnorm, "
-                   "aria_gelu_tanh, aria_add (both single-threaded in the reference), aria_rope_apply, "
-                   "aria_softmax_inplace on 1/8 of the score rows scaled x8; LayerNorm and the modulate "
-                   "glue via the restatement (no exported reference function)" % (reps, _cpu_model())),
+        "sample": ("one C2 step, warm-min of %d reps on the host CPU (%s, %d physical cores, OpenMP team %d, "
+                   "OMP_WAIT_POLICY=%s): reference aria_rmsnorm, aria_gelu_tanh, aria_add (both single-threaded "
+                   "in the reference), aria_rope_apply, aria_softmax_inplace on 1/8 of the score rows scaled x8; "
+                   "LayerNorm and the modulate glue via the restatement (no exported reference function)"
+                   % (reps, _cpu_model(), _physical_cores(), threads, os.environ.get("OMP_WAIT_POLICY"))),
         "ms_per_step": round(total * 1e3, 2),
         "ops_ms": {kk: round(v * 1e3, 3) for kk, v in best.items()},
+        "legs": legs,
     }
 
 
@@ -265,6 +355,12 @@ def main():
         ops_report[op] = {"us": round(avg * 1e3, 2), "GB/s": round(ab[op] / (avg * 1e-3) / 1e9, 1),
                           "bytes": ab[op], "frac_peak": round(ab[op] / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
 
+    # measured ceilings: empty-kernel floor and streaming copies of the same bytes
+    ceiling = ceiling_leg(L, chk, DeviceArray, time_loop, stream, reps)
+    for op in OPS:
+        ref = ceiling["copy_430MB" if op == "softmax" else "copy_42MB" if op == "rope" else "copy_21MB"]
+        ops_report[op]["frac_copy"] = round(ops_report[op]["GB/s"] / ref["GB/s"], 3)
+
     # extra: rot-32 RoPE (the DiT's), Q8/Q4 pack of W [4096, 1024]
     ms, _ = time_loop(lambda i: L.aria_hip_rope_apply2_dev(sets[i % len(sets)]["q"].p, sets[i % len(sets)]["k"].p,
                                                         d_cos.p, d_sin.p, B * H, S, HD, 32, stream), reps)
@@ -296,7 +392,7 @@ def main():
     dom_us = ops_report[dom]["us"]
     achieved = ab[dom] / (dom_us * 1e-6) / 1e9
     traffic = _pmc_traffic(dom)
-    cpu = None if args.no_cpu else cpu_baseline(x, sc, sh, w, q, k, cos64, sin64, scores)
+    cpu = None if args.no_cpu else cpu_baseline(x, sc, sh, w, q, k, cos64, sin64, scores, rng)
 
     line = {
         "metric": "fused-op HBM GB/s (% peak) + us per q4 DiT block at T=1296 on 1 MI355X",
@@ -320,6 +416,7 @@ def main():
                      "algorithmic_bytes": ab[dom], "avg_us": dom_us},
         "cpu_baseline": cpu,
         "ops": ops_report,
+        "ceiling": ceiling,
         "gemm": gemm,
         "block_us": block["gelu"]["us"],
         "block": block,
@@ -329,17 +426,48 @@ def main():
     print(json.dumps(line), flush=True)
 
 
+def ceiling_leg(L, chk, DeviceArray, time_loop, stream, reps):
+    """Measured ceilings of back-to-back launches on this box, the floor under every op's
+    figure: the empty-kernel time (a 64-float add, one workgroup), a streaming copy through the
+    library's elementwise kernel (y = x * 1.0: one read and one write per float) at the 21.2 MB
+    of one [2592, 1024] fp32 row op, the 42.5 MB of the RoPE pair and the 430 MB of the softmax,
+    and the runtime's device-to-device copy of the same bytes. Each through time_loop (median of
+    5 trials of back-to-back launches, HIP events on the launch stream)."""
+    out = {}
+    a, b = DeviceArray(64), DeviceArray(64)
+    ms, _ = time_loop(lambda i: L.aria_hip_add_dev(b.p, a.p, a.p, 64, stream), reps)
+    out["empty_us"] = round(ms * 1e3, 2)
+    for tag, nfloat in (("21MB", B * S * D), ("42MB", 2 * B * S * D), ("430MB", B * H * S * S)):
+        srcs = [DeviceArray(nfloat) for _ in range(2)]
+        dsts = [DeviceArray(nfloat) for _ in range(2)]
+        byt = 2 * nfloat * 4
+        ms, _ = time_loop(lambda i: L.aria_hip_scale_dev(dsts[i % 2].p, srcs[i % 2].p, 1.0, nfloat, stream), reps)
+        out["copy_" + tag] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / (ms * 1e-3) / 1e9, 1), "bytes": byt}
+        ms, _ = time_loop(lambda i: L.aria_hip_memcpy_d2d_async(dsts[i % 2].p, srcs[i % 2].p, nfloat * 4, stream), reps)
+        out["d2d_" + tag] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / (ms * 1e-3) / 1e9, 1), "bytes": byt}
+        for d in srcs + dsts:
+            d.free()
+    a.free(); b.free()
+    return out
+
+
 def gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps):
     """Config 3: X [2592,K] ~N(0,1) times W [N,K] ~N(0,0.02) packed on the device (bit-exact with
-    the reference quantizer), for (K,N) = (1024,4096) and (4096,1024), Q8 and Q4; w8a8 is the same
-    Q8 weight with the reference's W8A8 numbers (aria_linear_q8a8: per-row int8 quantisation of
-    the fp32 X, then the int8 MFMA GEMM; both launches timed, int8 ops counted as 2 M N K)."""
+    the reference quantizer), for (K,N) = (1024,4096) and (4096,1024), Q8 and Q4. The q8 / q4
+    entries take fp32 X as aria_linear_q8 / q4 do (aria_hip_qlinear_noalloc_dev: the fp16 staging
+    pass into the library's static scratch, then the MFMA GEMM; both launches timed); the
+    *_f16x entries are the GEMM alone on X already in fp16 (what the DiT block's producers
+    write). w8a8 is the same Q8 weight with the reference's W8A8 numbers (aria_linear_q8a8:
+    per-row int8 quantisation of the fp32 X, then the int8 MFMA GEMM; both launches timed, int8
+    ops counted as 2 M N K)."""
     out = {}
     M = B * S
     for K, N in ((1024, 4096), (4096, 1024)):
         Wh = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
         dW = DeviceArray.from_host(Wh)
-        dx = [DeviceArray.from_host(rng.standard_normal((M, K), dtype=np.float32)) for _ in range(2)]
+        xh = rng.standard_normal((M, K), dtype=np.float32)
+        dx = [DeviceArray.from_host(xh) for _ in range(2)]
+        dxh = [DeviceArray.from_host(xh.astype(np.float16)) for _ in range(2)]
         dy = DeviceArray((M, N))
         dq8, ds8 = DeviceArray((N, K), np.int8), DeviceArray(N, np.float32)
         dq4, ds4 = DeviceArray((N, K // 2), np.uint8), DeviceArray((N, 2 * K // 32), np.float32)
@@ -347,15 +475,16 @@ def gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps):
         chk(L.aria_hip_q4_quant_dev(dq4.p, ds4.p, dW.p, N, K, stream))
         flop = 2.0 * M * N * K
         for wt, (dq, ds) in ((0, (dq8, ds8)), (1, (dq4, ds4))):
-            fn = (lambda i, dq=dq, ds=ds, wt=wt: L.aria_hip_qlinear_dev(dy.p, 0, dx[i % 2].p, 0, wt, dq.p, ds.p,
-                                                                        None, M, K, N, stream))
-            for i in range(3):
-                chk(fn(i))
-            ms, ms_min = time_loop(fn, reps)
-            tf = flop / (ms * 1e-3) / 1e12
-            key = f"{'q8' if wt == 0 else 'q4'}_M{M}_K{K}_N{N}"
-            out[key] = {"us": round(ms * 1e3, 2), "us_min": round(ms_min * 1e3, 2), "TFLOP/s": round(tf, 1),
-                        "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 3), "flop": flop}
+            for suffix, xs, xf16 in (("", dx, 0), ("_f16x", dxh, 1)):
+                fn = (lambda i, dq=dq, ds=ds, wt=wt, xs=xs, xf16=xf16:
+                      L.aria_hip_qlinear_noalloc_dev(dy.p, 0, xs[i % 2].p, xf16, wt, dq.p, ds.p, None, M, K, N, stream))
+                for i in range(3):
+                    chk(fn(i))
+                ms, ms_min = time_loop(fn, reps)
+                tf = flop / (ms * 1e-3) / 1e12
+                key = f"{'q8' if wt == 0 else 'q4'}_M{M}_K{K}_N{N}{suffix}"
+                out[key] = {"us": round(ms * 1e3, 2), "us_min": round(ms_min * 1e3, 2), "TFLOP/s": round(tf, 1),
+                            "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 3), "flop": flop}
         wsb = int(L.aria_hip_q8a8_ws_bytes(M, K))
         dws = DeviceArray((wsb,), np.uint8)
         fn = (lambda i: L.aria_hip_linear_q8a8_dev(dy.p, dx[i % 2].p, 0, dq8.p, ds8.p, None, M, K, N, dws.p, stream))

@@ -272,25 +272,35 @@ def test_dit_create_rejects(hip):
         Dit(M, 2, 128, 4, 256, 16, 3, 32)     # head_dim 32
 
 
-def test_dit_config5_step(hip, port, R):
+def test_dit_config5_steps(hip, port, R):
     """Config 5 shape: 24 q4 blocks (config-4 block, tanh-GELU 4x FFN), T = 1296, batch 2,
-    latent [2, 64, 1296], context [2, 256, 1024]; one teacher-forced step of the 8 (the CPU side
-    costs ~48 block forwards per step), through the graph-captured batched step."""
+    latent [2, 64, 1296], context [2, 256, 1024], 8 pingpong steps on the reference's LogSNR
+    schedule (aria_build_schedule, src/aria_sampler.c:167-200) with per-step gcond and noise.
+    The device step runs every step (graph replay) and the latent advances by the host
+    pingpong update on the device velocity; at steps 0, 4 and 7 (the last) the CPU computes the
+    velocity from the same step input (teacher forcing, tests/test_quant_dit.c:1-7), ~48 block
+    forwards per checked step."""
     from aria_amd.dit import Dit, random_dit, FFN_GELU
-    depth, ed, H, inner, C, T, Sc, rot = 24, 1024, 16, 4096, 64, 1296, 256, 32
+    depth, ed, H, inner, C, T, Sc, rot, steps = 24, 1024, 16, 4096, 64, 1296, 256, 32, 8
     M = random_dit(rng(0xC5), depth, ed, inner, C, 0, ffn=FFN_GELU)
     c, s = R.rope_freqs(T, rot, 10000.0)
-    x, ced, g = inputs(0xC50, 2, C, T, Sc, ed)
+    x, ced, _ = inputs(0xC50, 2, C, T, Sc, ed)
+    r = rng(0xC51)
+    gall = randn(r, (steps, 2, 6 * ed), 0.1)
+    noise = randn(r, (steps,) + x.shape)
+    sched = R.build_schedule(steps)
     dit = Dit(M, depth, ed, H, inner, C, 0, rot, precision=4, ffn=FFN_GELU)
     dit.set_request(T, [ced[0], ced[1]], c, s)
-    dit.step(x, g)                       # captures
-    got = dit.step(x, g)                 # replays
-    assert dit.graph_active
-    for b in range(2):
-        want = ref_step(R, port, M, 4, x[b], ced[b], g[b], c, s, rot, H, ffn=FFN_GELU)
-        d = np.abs(got[b] - want)
-        print(f"config-5 step seq {b}: max|d| {d.max():.3e} max|ref| {np.abs(want).max():.3f}", flush=True)
-        assert_close(got[b], want, ATOL, RTOL, f"config-5 step seq {b}")
+    for i in range(steps):
+        v = dit.step(x, gall[i])
+        assert dit.graph_active
+        if i in (0, 4, 7):
+            for b in range(2):
+                want = ref_step(R, port, M, 4, x[b], ced[b], gall[i][b], c, s, rot, H, ffn=FFN_GELU)
+                d = np.abs(v[b] - want)
+                print(f"config-5 step {i} seq {b}: max|d| {d.max():.3e} max|ref| {np.abs(want).max():.3f}", flush=True)
+                assert_close(v[b], want, ATOL, RTOL, f"config-5 step {i} seq {b}")
+        x = port.pingpong(x, v, noise[i], float(sched[i]), float(sched[i + 1]))
     dit.free()
 
 
