@@ -31,7 +31,9 @@
 
 namespace {
 
-constexpr int KB = 64;   /* K-tile */
+constexpr int KB = 64;   /* K-tile (fp16 activations) */
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
 
 /* activation tile [BM][64] halves: 8 chunks of 16 B per row, logical chunk c of row r at
  * c ^ ((r >> 1) & 7) (conflict-free fragment reads: 32 rows x one chunk per lane half) */
@@ -107,8 +109,9 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t m0) {
 }
 
 /* Layout of one pipeline stage in LDS (bytes):
- *   [0, 128 BM)            activations [BM][64] fp16, chunk-swizzled (xo)
+ *   [0, 128 BM)            activations [BM][64] fp16 (W8A8: [BM][128] int8), chunk-swizzled (xo)
  *   Q8: [.., + 64 BN)      weights [BN][64] int8; 16 B chunk c of row r at c ^ ((r >> 2) & 3)
+ *   W8A8: [.., + 128 BN)   weights [BN][128] int8, chunk-swizzled as the activations
  *   Q4: [.., + 32 BN)      nibbles [BN][32 B]
  *       [.., + 4096)       [min, step] pairs of the K-tile, 16 B per row: wave w's 64 slots
  *                          at 1024 w (FN = 1: rows 32w.. in slots 0-31, 32-63 repeat them) */
@@ -116,11 +119,13 @@ template <int WT, int FM, int FN>
 struct Stage {
     static constexpr int BM = 32 * FM, BN = 128 * FN;
     static constexpr int A = BM * 128;
-    static constexpr int WQ = WT == ARIA_WQ8 ? BN * 64 : BN * 32;
-    static constexpr int WS = WT == ARIA_WQ8 ? 0 : 4096;
+    static constexpr int WQ = WT == ARIA_WI8 ? BN * 128 : WT == ARIA_WQ8 ? BN * 64 : BN * 32;
+    static constexpr int WS = WT == ARIA_WQ4 ? 4096 : 0;
     static constexpr int BYTES = A + WQ + WS;
     /* VMEM instructions one wave issues per K-tile */
-    static constexpr int DMA = FM + (WT == ARIA_WQ8 ? 2 * FN : FN + 1);
+    static constexpr int DMA = FM + (WT == ARIA_WI8 ? 4 * FN : WT == ARIA_WQ8 ? 2 * FN : FN + 1);
+    /* k per K-tile: 64 fp16 activations, or 128 int8 ones (W8A8), in the 128-byte rows */
+    static constexpr int KK = WT == ARIA_WI8 ? 128 : 64;
 };
 
 }  // namespace
@@ -145,11 +150,11 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
     if (t >= T) return;                     /* uniform per workgroup, before any barrier */
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lrow = lane & 31, lh = lane >> 5;
-    const int KT = a.K / (KB * NS);         /* pipeline steps */
+    const int KT = a.K / (St::KK * NS);     /* pipeline steps */
     uint32_t magic = 0x64006400u;           /* fp16 1024 in both halves, kept in a VGPR */
     asm volatile("" : "+v"(magic));
     const uint32_t sbase = (uint32_t)(uintptr_t)smem;
-    constexpr int NWQ = WT == ARIA_WQ8 ? 2 * FN : FN;   /* weight DMA instructions per wave */
+    constexpr int NWQ = WT == ARIA_WI8 ? 4 * FN : WT == ARIA_WQ8 ? 2 * FN : FN;   /* weight DMA per wave */
     const int rbase = wave * 32 * FN;                    /* this wave's first weight row */
 
     /* per-lane global sources of this wave's DMA slots for K-tile 0 of tile (m0, n0);
@@ -162,12 +167,18 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
         for (int i = 0; i < FM; i++) {
             const int p = 256 * i + 64 * wave + lane, r = p >> 3, cp = p & 7;
             const int c = cp ^ ((r >> 1) & 7);
-            xsrc[i] = (const uint16_t *)a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 8 * c;
+            if constexpr (WT == ARIA_WI8)   /* int8 rows: K bytes, 16 k per chunk */
+                xsrc[i] = reinterpret_cast<const uint16_t *>((const int8_t *)a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 16 * c);
+            else
+                xsrc[i] = (const uint16_t *)a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 8 * c;
         }
 #pragma unroll
         for (int i = 0; i < NWQ; i++) {
             const int p = 64 * i + lane;
-            if constexpr (WT == ARIA_WQ8) {
+            if constexpr (WT == ARIA_WI8) {
+                const int r = rbase + (p >> 3), c = (p & 7) ^ ((r >> 1) & 7);
+                wsrc[i] = (const uint8_t *)a.q + (size_t)min(n0 + r, a.N - 1) * a.K + 16 * c;
+            } else if constexpr (WT == ARIA_WQ8) {
                 const int r = rbase + (p >> 2), c = (p & 3) ^ ((r >> 2) & 3);
                 wsrc[i] = (const uint8_t *)a.q + (size_t)min(n0 + r, a.N - 1) * a.K + 16 * c;
             } else {
@@ -186,6 +197,14 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
         for (int u = 0; u < NS; u++) {
             const int k64 = NS * kt + u;
             const uint32_t st = sbase + B * SB + u * St::BYTES;
+            if constexpr (WT == ARIA_WI8) {   /* 128 int8 k per K-tile: 128 bytes of every row */
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+                    dma16(reinterpret_cast<const uint8_t *>(xsrc[i]) + k64 * 128, st + (256 * i + 64 * wave) * 16);
+#pragma unroll
+                for (int i = 0; i < NWQ; i++) dma16(wsrc[i] + k64 * 128, st + St::A + rbase * 128 + 1024 * i);
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < FM; i++) dma16(xsrc[i] + k64 * KB, st + (256 * i + 64 * wave) * 16);
             if constexpr (WT == ARIA_WQ8) {
@@ -200,7 +219,8 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
     };
     constexpr int DMA = NS * St::DMA;        /* VMEM instructions of one step */
 
-    f32x16_t acc[FM][FN];
+    using AccT = typename std::conditional<WT == ARIA_WI8, i32x16_t, f32x16_t>::type;
+    AccT acc[FM][FN];
 
     /* one K-tile from stage B: this lane's raw weights from LDS, then 4 MFMA steps of FM x FN
      * MFMAs; step ks + 1's activation fragments are requested and its weights unpacked while
@@ -209,6 +229,28 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
         constexpr int B = decltype(BB)::value;
         static_for<NS>([&](auto UU) __attribute__((always_inline)) {
         const uint8_t *S = smem + B * SB + decltype(UU)::value * St::BYTES;
+        if constexpr (WT == ARIA_WI8) {
+            /* W8A8: both operands straight from LDS, no unpack; lane half h covers k in
+             * [64 h, 64 h + 64) of the 128-k tile and step ks its 16 k at 64 h + 16 ks on both
+             * sides (the int32 sums are exact, so any common order gives the same bits) */
+            const uint16_t *X = reinterpret_cast<const uint16_t *>(S);
+            const uint16_t *Wr = reinterpret_cast<const uint16_t *>(S + St::A);
+            static_for<4>([&](auto KS) __attribute__((always_inline)) {
+                constexpr int ks = decltype(KS)::value;
+                i32x4_t xf[FM], wf[FN];
+#pragma unroll
+                for (int i = 0; i < FM; i++) xf[i] = *reinterpret_cast<const i32x4_t *>(&X[xo(i * 32 + lrow, 4 * lh + ks)]);
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    wf[j] = *reinterpret_cast<const i32x4_t *>(&Wr[xo(rbase + 32 * j + lrow, 4 * lh + ks)]);
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[j], xf[i], acc[i][j], 0, 0, 0);
+            });
+            return;
+        }
         const uint16_t *X = reinterpret_cast<const uint16_t *>(S);
         WSt<WT, FN> ws;
 #pragma unroll
@@ -292,7 +334,7 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
 #pragma unroll
         for (int j = 0; j < FN; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
     /* prologue: steps 0 .. PD - 1 in flight, then wait for step 0 */
     static_for<PD>([&](auto PP) __attribute__((always_inline)) {
         if (decltype(PP)::value < KT) issue(decltype(PP)::value, decltype(PP)::value);
@@ -309,7 +351,7 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
     /* every wave is past its last fragment read (the last step's barrier): the stages hold the
      * epilogue staging */
     float *E = reinterpret_cast<float *>(smem + wave * EPI_WAVE);
-    epilogue<FM, FN, WT, MODE, GELU>(a, acc, E, lane, m0, n0 + wave * 32 * FN);
+    epilogue<FM, FN, WT, MODE, GELU, AccT>(a, acc, E, lane, m0, n0 + wave * 32 * FN);
 }
 
 template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int NS = 1, int NST = 3>
@@ -367,5 +409,28 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
         default: return hipErrorInvalidValue;
     }
 #undef BIG_CASE
+    return hipGetLastError();
+}
+
+/* W8A8 (int8 activations, Q8 weights, K % 128 == 0): the configurations compiled, index = cfg,
+ * measured at M = 2592 against the weights-in-registers int8 kernel (k_gemm_i8.hip):
+ *   0: 64 x 128, two workgroups per CU: N <= 1024 (K = 1024: 14.6 -> 9.9 us; K = 4096: 39.4 -> 23.4 us)
+ *   1: 64 x 256: N <= 1024 with HEADS (a head's 64 columns in one wave)
+ *   2: 128 x 256: 1024 < N <= 3072 (the qkv projection: 22.2 -> 19.3 us) */
+#define BIG_I8_CFGS(X) X(0, 2, 1, 2) X(1, 2, 2, 1) X(2, 4, 2, 1)
+int qgemm_big_i8_ncfg() { return 3; }
+
+hipError_t qgemm_big_i8_launch(const QArgs &a, int cfg, hipStream_t s) {
+    if (a.K % 128 || (a.gelu && a.epi.mode != ARIA_EPI_STORE)) return hipErrorInvalidValue;
+#define BIG_I8_CASE(i, fm, fn, mb)                                                         \
+    case i:                                                                                \
+        if (a.epi.mode == ARIA_EPI_HEADS && fn < 2) return hipErrorInvalidValue;           \
+        launch_big<ARIA_WI8, fm, fn, mb>(a, s);                                            \
+        break;
+    switch (cfg) {
+        BIG_I8_CFGS(BIG_I8_CASE)
+        default: return hipErrorInvalidValue;
+    }
+#undef BIG_I8_CASE
     return hipGetLastError();
 }

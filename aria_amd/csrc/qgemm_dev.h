@@ -331,5 +331,8 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s);
 int qgemm_big_ncfg();
 int qgemm_big_bm(int cfg);
 int qgemm_big_bn(int cfg);
+/* its W8A8 form (int8 activations with per-row scales in a.xscale, Q8 weights, K % 128 == 0) */
+hipError_t qgemm_big_i8_launch(const QArgs &a, int cfg, hipStream_t s);
+int qgemm_big_i8_ncfg();
 
 #endif /* ARIA_QGEMM_DEV_H */
