@@ -129,6 +129,9 @@ SIGNATURES = {
     "aria_cuda_dec_medium_create": (_P, [_P]),
     "aria_cuda_dec_medium_free": (None, [_P]),
     "aria_cuda_dec_medium_forward": (None, [_P, _P, _P, _i]),
+    "aria_hip_dec_forward_dev": (_i, [_P, _P, _P, _i]),
+    "aria_hip_dec_stream": (_P, [_P]),
+    "aria_hip_dec_workspace_bytes": (_sz, [_P]),
     # include/aria_hip.h: host-pointer forms
     "aria_hip_linear_q8": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),
     "aria_hip_linear_q8a8": (_i, [_P, _P, _P, _P, _P, _i, _i, _i]),

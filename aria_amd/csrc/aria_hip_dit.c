@@ -1060,19 +1060,9 @@ int aria_cuda_dit_sample(aria_cuda_dit *h, float *x_CT, const float *sched, int 
 }
 
 /* ------------------------------------------------------------------------- */
-/* device decoders: not served here; NULL keeps the caller on its CPU decoder */
+/* the medium device decoder is not served: NULL keeps the caller on its CPU decoder  */
 /* ------------------------------------------------------------------------- */
 
-aria_cuda_dec *aria_cuda_dec_create(const aria_sa3_dec_view *v) {
-    (void)v;
-    aria_hip_set_error("aria_cuda_dec_create: the device decoder is not part of this backend");
-    return NULL;
-}
-void aria_cuda_dec_free(aria_cuda_dec *h) { (void)h; }
-void aria_cuda_dec_forward(aria_cuda_dec *h, float *audio, const float *latent, int T) {
-    (void)h; (void)audio; (void)latent; (void)T;
-    aria_hip_set_error("aria_cuda_dec_forward: no device decoder");
-}
 aria_cuda_dec_medium *aria_cuda_dec_medium_create(const aria_sa3_dec_medium_view *v) {
     (void)v;
     aria_hip_set_error("aria_cuda_dec_medium_create: the device decoder is not part of this backend");

@@ -175,6 +175,26 @@ hipError_t aria_k_sgemm(float *C, const float *A, const float *B, const float *b
 hipError_t aria_k_conv1d(float *out, const float *in, const float *w, const float *bias, int Cin,
                          int Cout, int K, int pad, int L, hipStream_t s);
 
+/* The small-music decoder's glue and attention (k_dec.hip); model dim 768, 12 heads of 64,
+ * 34-token chunks, 17-token groups.
+ *   dec_in:     xt fp16 [T, 256] = latent [256, T] * std, transposed
+ *   dec_expand: seq [Tp * 17, 768]: group t = x[t] (zeros for t >= T), then 16 new_tokens
+ *   dec_dyt:    y fp16 = tanh(alpha x) * g + b over [rows, 768]
+ *   dec_attn:   merged fp16 [nch * 34, 768] = the differential attention of each chunk from
+ *               qkv [nch * 34, 3840] (q | k | v | qd | kd), q/k DynamicTanh norms and RoPE
+ *               (rcos/rsin [34, 16]) applied inside
+ *   dec_im2col: xc fp32 [Lt, 2304] = the k3 mapping convolution's input rows
+ *   dec_out:    audio [2, Lt * 256] from mapped [Lt, 512] */
+hipError_t aria_k_dec_in(uint16_t *xt, const float *lat, int T, float std, hipStream_t s);
+hipError_t aria_k_dec_expand(float *seq, const float *x, const float *tok, int T, int Tp, hipStream_t s);
+hipError_t aria_k_dec_dyt(uint16_t *y, const float *x, float alpha, const float *g, const float *b, int rows,
+                          hipStream_t s);
+hipError_t aria_k_dec_attn(uint16_t *merged, const float *qkv, float qa, const float *qg, const float *qb,
+                           float ka, const float *kg, const float *kb, const float *rcos, const float *rsin,
+                           int nch, hipStream_t s);
+hipError_t aria_k_dec_im2col(float *xc, const float *seq, int Lt, int Lout, hipStream_t s);
+hipError_t aria_k_dec_out(float *audio, const float *mapped, int Lt, hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

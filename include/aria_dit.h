@@ -185,11 +185,26 @@ int aria_hip_dit_graph_active(const aria_cuda_dit *h);
  * next step). 0, or an error with the model unchanged. */
 int aria_hip_dit_load_overlay(aria_cuda_dit *h, const char *path);
 
-/* ---- device decoders (src/aria_sa3_dec.h:98-109): not served by this backend ----
- * create returns NULL (no fit), so the reference's caller keeps its CPU decoder
- * (src/aria_model_sa3.c:293-305, 634-647); free and forward accept only that NULL. */
+/* ---- device decoders (src/aria_sa3_dec.h:75-109) ----
+ * The small-music decoder runs on the device: aria_cuda_dec_create uploads the weight view
+ * (the reference's aria_sa3_dec_get_view fills it, src/aria_sa3_dec.c:299-318), and
+ * aria_cuda_dec_forward decodes latent [256, T] -> audio [2, T * 4096], host buffers,
+ * synchronous, as the reference's caller uses it (src/aria_model_sa3.c:293-305, 634-647).
+ * create returns NULL when there is no device or the weights do not fit (the caller keeps
+ * its CPU decoder). The medium decoder is not served: its create returns NULL.
+ * The two view types restate the reference's field for field (same order, same types), so
+ * a view filled by the reference's loader is read as is. */
 #ifndef ARIA_SA3_DEC_H
-typedef struct aria_sa3_dec_view aria_sa3_dec_view;
+typedef struct {
+    float pre_alpha, qn_alpha, kn_alpha, ff_alpha;
+    const float *pre_gamma, *pre_beta, *qn_gamma, *qn_beta, *kn_gamma, *kn_beta, *ff_gamma, *ff_beta;
+    const float *to_qkv, *to_out, *ff_in_w, *ff_in_b, *ff_out_w, *ff_out_b;
+} aria_taae_block_view;
+typedef struct {
+    float running_std;
+    const float *proj_w, *proj_b, *new_tokens, *mapping_w, *mapping_b;
+    aria_taae_block_view blocks[6];
+} aria_sa3_dec_view;
 typedef struct aria_sa3_dec_medium_view aria_sa3_dec_medium_view;
 typedef struct aria_cuda_dec aria_cuda_dec;
 typedef struct aria_cuda_dec_medium aria_cuda_dec_medium;
@@ -200,6 +215,14 @@ aria_cuda_dec_medium *aria_cuda_dec_medium_create(const aria_sa3_dec_medium_view
 void aria_cuda_dec_medium_free(aria_cuda_dec_medium *h);
 void aria_cuda_dec_medium_forward(aria_cuda_dec_medium *h, float *audio, const float *latent, int T);
 #endif
+
+/* ---- decoder extension: the decode on device buffers ----
+ * latent [256, T] and audio [2, T * 4096] in HBM, enqueued on the handle's stream
+ * (aria_hip_dec_stream) and not waited for; 0 or a negative ARIA_HIP_E* code. */
+int aria_hip_dec_forward_dev(aria_cuda_dec *h, float *daudio, const float *dlatent, int T);
+void *aria_hip_dec_stream(const aria_cuda_dec *h);
+/* device bytes of the decode workspace (grown to the longest T decoded so far) */
+size_t aria_hip_dec_workspace_bytes(const aria_cuda_dec *h);
 
 #ifdef __cplusplus
 }

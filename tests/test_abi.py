@@ -111,12 +111,16 @@ LAYOUT_FIELDS = {
                               "cross_v", "cross_kd", "cross_ed", "local_emb", "has_local", "steer"],
     "aria_steer": ["site", "op", "layer", "dir", "dim", "dir_norm2", "scale", "step_lo", "step_hi"],
     "aria_steer_set": ["items", "n"],
+    "aria_taae_block_view": ["pre_alpha", "qn_alpha", "kn_alpha", "ff_alpha", "pre_gamma", "pre_beta", "qn_gamma",
+                             "qn_beta", "kn_gamma", "kn_beta", "ff_gamma", "ff_beta", "to_qkv", "to_out", "ff_in_w",
+                             "ff_in_b", "ff_out_w", "ff_out_b"],
+    "aria_sa3_dec_view": ["running_std", "proj_w", "proj_b", "new_tokens", "mapping_w", "mapping_b", "blocks"],
 }
 DTYPE_VALUES = ["ARIA_F32", "ARIA_F16", "ARIA_BF16", "ARIA_Q8", "ARIA_Q4", "ARIA_Q8A8", "ARIA_DTYPE_AUTO"]
 
 
-def _layout_program(include):
-    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{include}"', "int main(void) {"]
+def _layout_program(includes):
+    lines = ["#include <stdio.h>", "#include <stddef.h>"] + [f'#include "{h}"' for h in includes] + ["int main(void) {"]
     for t, fields in LAYOUT_FIELDS.items():
         lines.append(f'    printf("{t} %zu\\n", sizeof({t}));')
         for f in fields:
@@ -128,9 +132,9 @@ def _layout_program(include):
     return "\n".join(lines) + "\n"
 
 
-def _layout(tmp_path, tag, include, incdir):
+def _layout(tmp_path, tag, includes, incdir):
     src = tmp_path / f"layout_{tag}.c"
-    src.write_text(_layout_program(include))
+    src.write_text(_layout_program(includes))
     exe = tmp_path / f"layout_{tag}"
     subprocess.run(["gcc", "-std=c11", "-D_GNU_SOURCE", "-w", "-I", incdir, str(src), "-o", str(exe)], check=True)
     return subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines()
@@ -143,15 +147,16 @@ def test_struct_layouts(tmp_path):
     """The restated reference types are byte-compatible: every field's offset and size, each
     type's size and the aria_dtype values, compiled from include/aria_dit.h and from the
     reference's own headers (src/aria_sa3_dit.h:40-48, 128-145, src/aria_steer.h:26-38,
-    src/aria_quant.h:27-35) by the same program. Where the reference tree is absent (the GPU
-    box) the sizes measured from it are checked instead."""
-    mine = _layout(tmp_path, "mine", "aria_dit.h", os.path.join(ROOT, "include"))
+    src/aria_quant.h:27-35, src/aria_sa3_dec.h:75-84) by the same program. Where the reference
+    tree is absent (the GPU box) the sizes measured from it are checked instead."""
+    mine = _layout(tmp_path, "mine", ["aria_dit.h"], os.path.join(ROOT, "include"))
     if os.path.exists(os.path.join(REF_SRC, "aria_sa3_dit.h")):
-        theirs = _layout(tmp_path, "ref", "aria_sa3_dit.h", REF_SRC)
+        theirs = _layout(tmp_path, "ref", ["aria_sa3_dit.h", "aria_sa3_dec.h"], REF_SRC)
         assert mine == theirs, [(a, b) for a, b in zip(mine, theirs) if a != b]
     got = dict(ln.rsplit(" ", 1) if ln.count(" ") == 1 else (ln, "") for ln in mine)
     assert [int(got[t]) for t in ("aria_dit_block_w", "aria_sa3_dit_view", "aria_sa3_dit_req_view", "aria_steer",
-                                  "aria_steer_set", "aria_dtype")] == [168, 88, 96, 48, 16, 4]
+                                  "aria_steer_set", "aria_taae_block_view", "aria_sa3_dec_view", "aria_dtype")] \
+        == [168, 88, 96, 48, 16, 128, 816, 4]
 
 
 def test_reference_callers_link_against_backend(libpath):

@@ -1,0 +1,101 @@
+"""GPU parity of the device small-music decoder (aria_cuda_dec_create / _forward, the reference's
+src/aria_sa3_dec.h:98-109) against the reference's own CPU decoder, compiled from its sources
+(aria_sa3_dec_forward, src/aria_sa3_dec.c:118-128) and loaded by its own loader from a random-init
+checkpoint with the reference's tensor names.
+
+The device decoder is created from the view the reference's loader fills
+(aria_sa3_dec_get_view), exactly as the reference's caller does (src/aria_model_sa3.c:293-305).
+Gate: the reference's decoder gate, max|d| <= 1e-3 + 5e-3 * max|ref| (tests/test_dec.c:118-125),
+plus a relative rms error <= 1e-3: the device keeps the GEMM operands in fp16, as the
+reference's device decoder does, and a numpy emulation of that rounding measures ~1.2e-4 at
+these weights, so the rms bound leaves 8x headroom while a wrong index, sign or halo moves
+it by O(1).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL, RMS = 1e-3, 5e-3, 1e-3
+
+
+@pytest.fixture(scope="module")
+def model(tmp_path_factory, hip):
+    import oracle
+    from oracle import dec as odec
+    R = oracle.ref()
+    if R is None:
+        pytest.skip("oracle/_ref not built: the decoder oracle is the compiled reference")
+    t = odec.random_tensors(rng(7))
+    path = str(tmp_path_factory.mktemp("dec") / "dec.safetensors")
+    odec.write_safetensors(path, t)
+    rd = odec.RefDecoder(R.lib, path)
+    from aria_amd.dec import Decoder
+    print("[gpu] aria_cuda_dec_create (reference view)", flush=True)
+    dv = Decoder(rd.view())
+    yield rd, dv, t
+    dv.free()
+    rd.close()
+
+
+def _rms_rel(got, ref):
+    d = np.asarray(got, np.float64) - ref
+    return float(np.sqrt(np.mean(d * d) / np.mean(np.asarray(ref, np.float64) ** 2)))
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 8, 37, 108])
+def test_dec_matches_reference_decoder(model, T):
+    """odd T pads one frame (src/aria_sa3_dec.c:67); T = 1 leaves the shifted pass one chunk of
+    halo plus data; T = 108 is a 10 s clip"""
+    rd, dv, _ = model
+    lat = rng(100 + T).standard_normal((256, T)).astype(np.float32)
+    print(f"[gpu] decoder T={T}", flush=True)
+    got = dv.forward(lat)
+    want = rd.forward(lat)
+    assert got.shape == (2, T * 4096) and np.isfinite(got).all()
+    assert_close(got, want, ATOL, RTOL, f"decoder T={T}")
+    assert _rms_rel(got, want) <= RMS, _rms_rel(got, want)
+
+
+def test_dec_device_buffers_match_host_entry(model, hip):
+    """aria_hip_dec_forward_dev on HBM buffers gives the host entry's audio bit for bit; the
+    workspace grows for a longer latent and is reused for a shorter one, with the same results"""
+    from aria_amd.device import DeviceArray, sync
+    _, dv, _ = model
+    for T in (9, 40, 3):
+        lat = rng(200 + T).standard_normal((256, T)).astype(np.float32)
+        print(f"[gpu] decoder dev T={T}", flush=True)
+        want = dv.forward(lat)
+        dl = DeviceArray.from_host(lat)
+        da = DeviceArray((2, T * 4096))
+        dv.forward_dev(da.p, dl.p, T)
+        sync(dv.stream)
+        assert np.array_equal(da.to_host(), want)
+        assert np.array_equal(dv.forward(lat), want)   # deterministic
+    assert dv.workspace_bytes() > 0
+
+
+def test_dec_from_checkpoint_tensors(model):
+    """a view built from the checkpoint tensors (view_from_tensors: the mapping conv folded as the
+    reference's loader folds it) decodes bit-identically to the reference loader's view"""
+    from aria_amd.dec import Decoder
+    _, dv, t = model
+    lat = rng(300).standard_normal((256, 6)).astype(np.float32)
+    d2 = Decoder.from_tensors(t)
+    try:
+        assert np.array_equal(d2.forward(lat), dv.forward(lat))
+    finally:
+        d2.free()
+
+
+def test_dec_rejects_bad_arguments(model, hip):
+    L = hip.lib()
+    _, dv, _ = model
+    assert L.aria_hip_dec_forward_dev(dv.h, None, None, 4) == -1
+    assert L.aria_hip_dec_forward_dev(dv.h, 1 << 20, 1 << 20, 0) == -1
+    assert not L.aria_cuda_dec_create(None)
+    assert not L.aria_cuda_dec_medium_create(None)

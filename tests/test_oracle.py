@@ -446,3 +446,68 @@ def test_block_composition_q8a8(port, R):
     q8 = DB.block_forward(R, port, x, kc, vc, gcond, W, DB.pack_weights(R, W, "q8"), c, s, 32, H, DB.FFN_GLU)
     e_q8 = np.abs((q8 - x) - (want - x)).max() / np.abs(want - x).max()
     assert e8 <= 0.06 and e_q8 < 0.1 * e8, (e8, e_q8)
+
+
+# ---------------------------------------------------------------- the small-music decoder
+
+@pytest.fixture(scope="module")
+def dec_model(tmp_path_factory):
+    import oracle
+    from oracle import dec as odec
+    R = oracle.ref()
+    if R is None:
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    t = odec.random_tensors(rng(7))
+    path = str(tmp_path_factory.mktemp("dec") / "dec.safetensors")
+    odec.write_safetensors(path, t)
+    rd = odec.RefDecoder(R.lib, path)
+    yield rd, t
+    rd.close()
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 6])
+def test_decoder_restatement_pinned_to_reference(dec_model, T):
+    """oracle/dec.py's numpy decoder (the stage checker) against the reference's own compiled
+    aria_sa3_dec_forward, loaded by its own loader from the same file: agreement to float32
+    reassociation (GEMM order) across odd/even T, the pad frame and both chunk passes; a
+    plausible mistake -- value and gate halves of the GLU swapped -- is far outside it."""
+    from oracle import dec as odec
+    rd, t = dec_model
+    lat = rng(50 + T).standard_normal((256, T)).astype(np.float32)
+    want = rd.forward(lat)
+    assert_close(odec.decode_np(t, lat), want, 1e-5, 1e-5, f"decode_np T={T}")
+    bad = dict(t)
+    for i in range(6):
+        k = odec.BLK % i + "ff.ff.0.proj."
+        for s in ("weight", "bias"):
+            a = t[k + s]
+            bad[k + s] = np.concatenate([a[odec.INNER:], a[:odec.INNER]])
+    assert np.abs(odec.decode_np(bad, lat) - want).max() > 1e-2 * np.abs(want).max()
+
+
+def test_decoder_view_matches_reference_loader(dec_model):
+    """aria_amd.dec.view_from_tensors (the host side of aria_cuda_dec_create for a caller
+    without the reference's loader) gives the view aria_sa3_dec_get_view gives: equal
+    scalars, equal arrays behind every pointer, and the folded mapping conv bit-exact."""
+    import ctypes as C
+    from aria_amd.dec import view_from_tensors
+    rd, t = dec_model
+    a = rd.view()
+    b, keep = view_from_tensors(t)
+
+    def arr(p, n):
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(n,)).copy()
+
+    assert a.running_std == b.running_std
+    for f, n in (("proj_w", 768 * 256), ("proj_b", 768), ("new_tokens", 768), ("mapping_w", 512 * 2304),
+                 ("mapping_b", 512)):
+        assert np.array_equal(arr(getattr(a, f), n), arr(getattr(b, f), n)), f
+    sizes = {"pre_gamma": 768, "pre_beta": 768, "qn_gamma": 64, "qn_beta": 64, "kn_gamma": 64, "kn_beta": 64,
+             "ff_gamma": 768, "ff_beta": 768, "to_qkv": 3840 * 768, "to_out": 768 * 768,
+             "ff_in_w": 4608 * 768, "ff_in_b": 4608, "ff_out_w": 768 * 2304, "ff_out_b": 768}
+    for i in range(6):
+        for f in ("pre_alpha", "qn_alpha", "kn_alpha", "ff_alpha"):
+            assert getattr(a.blocks[i], f) == getattr(b.blocks[i], f)
+        for f, n in sizes.items():
+            assert np.array_equal(arr(getattr(a.blocks[i], f), n), arr(getattr(b.blocks[i], f), n)), (i, f)
+    del keep
