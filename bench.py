@@ -205,6 +205,21 @@ def cpu_baseline(x, sc, sh, w, q, k, cos64, sin64, scores, rng):
     legs["c4"] = {"block_us": round(tb * 2 * 1e6, 0), "per_sequence_ms": round(tb * 1e3, 1),
                   "sample": "one sequence of T = 1296 (the reference block is batch 1), one warm + one timed "
                             "forward, x2 for the CFG pair; the per-request cross K/V projection excluded, as on the GPU"}
+
+    # F4: the reference's CPU decoder (aria_sa3_dec_forward, loaded by its own loader from a
+    # synthetic checkpoint) at T = 108, 10 s of audio
+    import tempfile
+    from oracle import dec as odec
+    from aria_amd.dec import random_tensors
+    with tempfile.TemporaryDirectory() as td:
+        pth = os.path.join(td, "dec.safetensors")
+        odec.write_safetensors(pth, random_tensors(rng))
+        if kind == "reference":
+            with odec.RefDecoder(R.lib, pth) as rd:
+                lat = rng.standard_normal((256, 108), dtype=np.float32)
+                td_s = _warm_min(lambda: rd.forward(lat), 2)
+            legs["f4"] = {"T108_ms": round(td_s * 1e3, 1), "x_realtime": round(108 * 4096 / 44100 / td_s, 1),
+                          "sample": "full size (T = 108, 10 s of audio), warm-min of 2"}
     return {
         "value": round(sum(ab.values()) / total / 1e9, 2),
         "unit": "GB/s",
@@ -387,6 +402,8 @@ def main():
     block = block_leg(DeviceArray, time_loop, stream, rng, reps)
     # C5: 24-block q4 stack x 8 steps, graph replay vs inline, and the device sampler
     dit = None if args.no_dit else dit_leg(DeviceArray, Timer, L, chk, stream, rng)
+    # F4: the device small-music decoder at 10 s and 60 s of audio
+    dec = dec_leg(DeviceArray, Timer, rng)
 
     dom = max(OPS, key=lambda o: ops_report[o]["us"])
     dom_us = ops_report[dom]["us"]
@@ -421,6 +438,7 @@ def main():
         "block_us": block["gelu"]["us"],
         "block": block,
         "dit": dit,
+        "dec": dec,
         "wall_s_timed": round(t_wall, 3),
     }
     print(json.dumps(line), flush=True)
@@ -533,6 +551,43 @@ def block_leg(DeviceArray, time_loop, stream, rng, reps):
                      "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "flop": flop,
                      "weight_bytes": blk.weight_bytes}
         blk.free()
+    return out
+
+
+def dec_leg(DeviceArray, Timer, rng, reps=10):
+    """F4: the device small-music decoder (random-init weights of the reference's architecture,
+    latent ~N(0,1)) at T = 108 (10 s of audio) and T = 646 (60 s): latent and audio resident in
+    HBM, aria_hip_dec_forward_dev back to back on the decoder's stream, HIP events on that
+    stream. The flop count is the GEMMs' (2 * rows * K * N over the six blocks' four
+    projections, the input projection and the mapping convolution) plus the chunk attention's
+    four 34 x 34 x 64 products per (chunk, head)."""
+    from aria_amd.dec import Decoder, random_tensors
+    d = Decoder.from_tensors(random_tensors(rng))
+    out = {}
+    for T in (108, 646):
+        lat = DeviceArray.from_host(rng.standard_normal((256, T), dtype=np.float32))
+        aud = DeviceArray((2, T * 4096))
+        for _ in range(3):
+            d.forward_dev(aud.p, lat.p, T)
+        res = []
+        for _ in range(3):
+            tm = Timer(d.stream)
+            tm.start()
+            for _ in range(reps):
+                d.forward_dev(aud.p, lat.p, T)
+            res.append(tm.stop() / reps)
+        ms = statistics.median(res)
+        Tp = T + (T & 1)
+        rows = 3 * 17 * Tp + 3 * (17 * Tp + 34)
+        nch = 3 * (Tp // 2) + 3 * (Tp // 2 + 1)
+        flop = 2.0 * rows * 768 * (3840 + 768 + 4608) + 2.0 * rows * 2304 * 768 + 2.0 * T * 256 * 768 \
+            + 2.0 * 16 * T * 2304 * 512 + nch * 12 * 4 * 2.0 * 34 * 34 * 64
+        out[f"T{T}"] = {"ms": round(ms, 3), "audio_s": round(T * 4096 / 44100, 1),
+                        "x_realtime": round(T * 4096 / 44100 / (ms * 1e-3), 0),
+                        "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "flop": flop}
+        del lat, aud
+    out["workspace_MiB"] = round(d.workspace_bytes() / 2 ** 20, 1)
+    d.free()
     return out
 
 

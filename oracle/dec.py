@@ -9,8 +9,8 @@
   and taae_block_forward / taae_chunk_pass (src/aria_taae.c:93-205), pinned against
   RefDecoder in tests/test_oracle.py; its stage outputs (``stages=True``) locate a
   device mismatch.
-* ``random_tensors``  a synthetic checkpoint with the reference's tensor names and shapes
-  (no checkpoint is available here).
+The synthetic checkpoints come from aria_amd.dec.random_tensors (the reference's tensor
+names and shapes; no checkpoint is available here).
 
 Only tests/ and bench.py's cpu_baseline leg use this module.
 """
@@ -25,61 +25,6 @@ import numpy as np
 D, H, HD, ROT, INNER, QKV, S = 768, 12, 64, 32, 2304, 3840, 34
 PFX = "pretransform.model."
 BLK = PFX + "decoder.layers.3.transformers.%d."
-
-
-def tensor_shapes():
-    """name -> shape, as aria_sa3_dec_load reads them (src/aria_sa3_dec.c:242-266)."""
-    sh = {PFX + "bottleneck.running_std": (1,),
-          PFX + "decoder.layers.1.weight": (D, 256), PFX + "decoder.layers.1.bias": (D,),
-          PFX + "decoder.layers.3.new_tokens": (D,),
-          PFX + "decoder.layers.3.mapping.weight_g": (512, 1, 1),
-          PFX + "decoder.layers.3.mapping.weight_v": (512, D, 3),
-          PFX + "decoder.layers.3.mapping.bias": (512,)}
-    for i in range(6):
-        for n in ("pre_norm", "self_attn.q_norm", "self_attn.k_norm", "ff_norm"):
-            dim = HD if "attn" in n else D
-            sh[BLK % i + n + ".alpha"] = (1,)
-            sh[BLK % i + n + ".gamma"] = (dim,)
-            sh[BLK % i + n + ".beta"] = (dim,)
-        sh[BLK % i + "self_attn.to_qkv.weight"] = (QKV, D)
-        sh[BLK % i + "self_attn.to_out.weight"] = (D, D)
-        sh[BLK % i + "ff.ff.0.proj.weight"] = (2 * INNER, D)
-        sh[BLK % i + "ff.ff.0.proj.bias"] = (2 * INNER,)
-        sh[BLK % i + "ff.ff.2.weight"] = (D, INNER)
-        sh[BLK % i + "ff.ff.2.bias"] = (D,)
-    return sh
-
-
-def random_tensors(rng, qk_gain=2.0):
-    """Random-init weights of the decoder's architecture, scaled so activations stay O(1)
-    through the six blocks: Linear weights ~ N(0, 1/fan_in) (residual outputs halved), DyT
-    alpha in [0.5, 1.5], gamma ~ 1, beta small; the q/k norm gains qk_gain make the
-    attention peaked enough that position (RoPE) and chunking matter."""
-    t = {}
-    for name, shape in tensor_shapes().items():
-        if name.endswith(".alpha"):
-            a = rng.uniform(0.5, 1.5, shape)
-        elif name.endswith(".gamma"):
-            g = qk_gain if "_norm.gamma" in name and "attn" in name else 1.0
-            a = g * (1.0 + 0.1 * rng.standard_normal(shape))
-        elif name.endswith(".beta") or name.endswith(".bias"):
-            a = 0.05 * rng.standard_normal(shape)
-        elif name.endswith("running_std"):
-            a = np.array([0.9])
-        elif name.endswith("new_tokens"):
-            a = 0.5 * rng.standard_normal(shape)
-        elif name.endswith("weight_g"):
-            a = rng.uniform(0.5, 1.5, shape)
-        elif name.endswith("weight_v"):
-            a = rng.standard_normal(shape)
-        else:   # Linear [out, in]
-            fan_in = shape[1]
-            s = 1.0 / np.sqrt(fan_in)
-            if "to_out" in name or "ff.ff.2" in name:
-                s *= 0.5
-            a = s * rng.standard_normal(shape)
-        t[name] = np.ascontiguousarray(a, np.float32)
-    return t
 
 
 def write_safetensors(path, tensors):

@@ -30,7 +30,8 @@ def model(tmp_path_factory, hip):
     R = oracle.ref()
     if R is None:
         pytest.skip("oracle/_ref not built: the decoder oracle is the compiled reference")
-    t = odec.random_tensors(rng(7))
+    from aria_amd.dec import random_tensors
+    t = random_tensors(rng(7))
     path = str(tmp_path_factory.mktemp("dec") / "dec.safetensors")
     odec.write_safetensors(path, t)
     rd = odec.RefDecoder(R.lib, path)

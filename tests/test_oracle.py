@@ -457,7 +457,8 @@ def dec_model(tmp_path_factory):
     R = oracle.ref()
     if R is None:
         pytest.skip("oracle/_ref not built (reference sources absent)")
-    t = odec.random_tensors(rng(7))
+    from aria_amd.dec import random_tensors
+    t = random_tensors(rng(7))
     path = str(tmp_path_factory.mktemp("dec") / "dec.safetensors")
     odec.write_safetensors(path, t)
     rd = odec.RefDecoder(R.lib, path)
