@@ -25,8 +25,7 @@
  *     g16    = silu(gate) * value of h16 . ff_in^T + b k_qgemm (GLU epilogue)
  *     seq   += g16 . ff_out^T + b                      k_qgemm (ADD epilogue)
  *   xc   = im2col of the last 16 of each group          k_dec_im2col (first T * 16 rows)
- *   mapped = xc . mapping^T + b                        k_sgemm (fp32)
- *   audio  = unpatch(mapped)                           k_dec_out
+ *   audio = unpatch(xc . mapping^T + b)                 k_dec_map (fp32 MFMA)
  * The workspace is kept on the handle and grown when a longer latent arrives.
  */
 #define __HIP_PLATFORM_AMD__ 1
@@ -206,11 +205,11 @@ aria_cuda_dec *aria_cuda_dec_create(const aria_sa3_dec_view *v) {
  *   seq   [L + 34, 768] f32   (the sequence at row 17; halos at rows 0-16, L + 17 ..)
  *   h16   [L + 34, 768] f16   m16 [L + 34, 768] f16
  *   qkv   [L + 34, 3840] f32  (after the blocks: xc [T * 16, 2304] f32)
- *   g16   [L + 34, 2304] f16  (after the blocks: mapped [T * 16, 512] f32)
+ *   g16   [L + 34, 2304] f16
  *   audio [2, T * 4096] f32
  * L = 17 * Tp, Tp = T rounded up to even. */
 typedef struct {
-    float *lat, *x, *seq, *qkv, *xc, *mapped, *audio;
+    float *lat, *x, *seq, *qkv, *xc, *audio;
     uint16_t *xt16, *h16, *m16, *g16;
 } dec_ws;
 
@@ -232,7 +231,6 @@ static size_t ws_layout(int T, dec_ws *w, char *base) {
 #undef CARVE
     if (w) {
         w->xc = w->qkv;                   /* Lt * 2304 * 4 <= R * 3840 * 4 */
-        w->mapped = (float *)w->g16;      /* Lt * 512 * 4 <= R * 2304 * 2 */
     }
     return off;
 }
@@ -281,9 +279,7 @@ static int dec_run(aria_cuda_dec *h, const dec_ws *w, float *audio, const float 
     for (int i = 3; i < 6; i++)
         if ((rc = block(h, &h->blk[i], w, w->seq, L / DS + 1, s))) return rc;
     STEP(aria_k_dec_im2col(w->xc, seq, Lt, Lout, s), "k_dec_im2col");
-    STEP(aria_k_sgemm(w->mapped, w->xc, h->mapping_w, h->mapping_b, Lt, DOUT, 3 * DD, 1, 1.0f, 1, 0, 0, 0, s),
-         "k_sgemm (decoder mapping)");
-    STEP(aria_k_dec_out(audio, w->mapped, Lt, s), "k_dec_out");
+    STEP(aria_k_dec_map(audio, w->xc, h->mapping_w, h->mapping_b, Lt, s), "k_dec_map (mapping + unpatch)");
     return 0;
 }
 

@@ -184,7 +184,7 @@ hipError_t aria_k_conv1d(float *out, const float *in, const float *w, const floa
  *               qkv [nch * 34, 3840] (q | k | v | qd | kd), q/k DynamicTanh norms and RoPE
  *               (rcos/rsin [34, 16]) applied inside
  *   dec_im2col: xc fp32 [Lt, 2304] = the k3 mapping convolution's input rows
- *   dec_out:    audio [2, Lt * 256] from mapped [Lt, 512] */
+ *   dec_map:    audio [2, M * 256] = unpatch(xc [M, 2304] . W [512, 2304]^T + b), fp32 MFMA */
 hipError_t aria_k_dec_in(uint16_t *xt, const float *lat, int T, float std, hipStream_t s);
 hipError_t aria_k_dec_expand(float *seq, const float *x, const float *tok, int T, int Tp, hipStream_t s);
 hipError_t aria_k_dec_dyt(uint16_t *y, const float *x, float alpha, const float *g, const float *b, int rows,
@@ -193,7 +193,7 @@ hipError_t aria_k_dec_attn(uint16_t *merged, const float *qkv, float qa, const f
                            float ka, const float *kg, const float *kb, const float *rcos, const float *rsin,
                            int nch, hipStream_t s);
 hipError_t aria_k_dec_im2col(float *xc, const float *seq, int Lt, int Lout, hipStream_t s);
-hipError_t aria_k_dec_out(float *audio, const float *mapped, int Lt, hipStream_t s);
+hipError_t aria_k_dec_map(float *audio, const float *xc, const float *W, const float *b, int M, hipStream_t s);
 
 #ifdef __cplusplus
 }

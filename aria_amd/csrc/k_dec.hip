@@ -8,14 +8,16 @@
  *   k_dec_in      softnorm inverse and transpose: latent [256, T] * std -> fp16 [T, 256]
  *   k_dec_expand  the 17-token groups: frame t's projected token, then 16 new_tokens
  *   k_dec_dyt     DynamicTanh norm tanh(alpha x) * gamma + beta -> fp16 GEMM operand
- *   k_dec_attn    one chunk-head of the differential self-attention, fused: the q/k
+ *   k_dec_attn_mfma  one chunk-head of the differential self-attention, fused: the q/k
  *                 DynamicTanh norms, RoPE (32 rotated dims), both softmax(q k^T / 8) v
- *                 products over the chunk's 34 tokens, their difference, merged fp16
- *   k_dec_im2col  the k = 3 mapping convolution's input rows (the last 16 of each group),
- *                 fp32: the mapping runs as an fp32 GEMM, as the reference keeps it
- *   k_dec_out     trim to T * 16 and unpatch to stereo: audio[c][l * 256 + i]
- * Arithmetic follows the reference's order (built with -ffp-contract=off); tanhf is the
- * device library's, the softmax exponential v_exp_f32 (~1 ulp).
+ *                 products over the chunk's 34 tokens on the fp32 MFMA, their difference,
+ *                 merged fp16
+ *   k_dec_im2col  the k = 3 mapping convolution's input rows (the last 16 of each group)
+ *   k_dec_map     the mapping convolution as an fp32 GEMM on the fp32 MFMA (the reference
+ *                 keeps it fp32), trimmed to T * 16 rows and unpatched to stereo in its stores
+ * Arithmetic follows the reference's order (built with -ffp-contract=off); the DyT norms use
+ * the device library's tanhf, the attention's q/k norms tanh_fast (exp + rcp, a few 1e-7
+ * absolute) and the softmax exponential v_exp_f32 (~1 ulp).
  */
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
@@ -78,93 +80,172 @@ struct DecAttnArgs {
     const float *rcos, *rsin;   /* [34, 16] */
 };
 
-/* One (chunk, head) per workgroup of two waves; wave w computes the attention of pair w
- * (0: q, k; 1: qd, kd) with lane i < 34 owning query row i: its normalised, rotated q row
- * stays in registers, the chunk's k rows (normalised, rotated) and v rows sit in LDS and
- * are read as broadcasts (every lane the same address). Scores in registers, softmax per
- * lane, then o = P v. The difference ob - od goes out as the merged fp16 row
- * (src/aria_taae.c:116-133). */
-__global__ __launch_bounds__(128) void k_dec_attn(DecAttnArgs a, int H) {
-    __shared__ float sk[2][DEC_S][DEC_HD];
-    __shared__ float sv[DEC_S][DEC_HD];
-    __shared__ float sod[DEC_S][DEC_HD + 1];
+/* ---- the chunk attention on the fp32 MFMA (v_mfma_f32_16x16x4_f32) ----
+ * One (chunk, head) per workgroup of two waves; wave w computes pair w (0: q, k; 1: qd, kd)
+ * over the chunk's 34 tokens padded to 48 (3 blocks of 16):
+ *   S = q k^T: 3 x 3 blocks, 16 k-steps; lane l supplies row l % 16 of q (A) and of k (B) at
+ *     dim 16 (l / 16) + s in step s, so each lane loads 16 consecutive dims of one row from
+ *     qkv, applies the DynamicTanh norm and RoPE in registers (the rotation's partner dim
+ *     d +- 16 sits in lane l ^ 16, same row) and keeps them as its operands
+ *   softmax over the 34 valid keys in the accumulators (a row's 16 columns of a block sit in
+ *     16 lanes: xor-shuffle reductions), probabilities through LDS into the A layout
+ *   O = P v: 3 x 4 blocks, 12 k-steps over keys 12 (l / 16) + s, v read from qkv
+ * Wave 1 leaves O in LDS (lane-major), wave 0 writes half(O0 - O1) to the merged rows.
+ * Accumulator v of lane l in a 16 x 16 block: row 4 (l / 16) + v, column l % 16. Padded q / k
+ * rows are zero and padded keys are masked before the max, so nothing past the chunk's rows
+ * is read. fp32 operands, as the reference keeps this attention fp32. */
+#define DA_P 48            /* padded chunk */
+#define DA_PS 52           /* LDS row stride of P (floats; 16-byte aligned rows) */
+
+typedef float f32x4_dec __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
+    __shared__ __attribute__((aligned(16))) float Ps[2][DA_P * DA_PS];
+    __shared__ float Os[48 * 64];
     const int ch = blockIdx.x / H, h = blockIdx.x % H;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int lr = lane & 15, lq = lane >> 4;
     const float *base = a.qkv + (size_t)ch * DEC_S * DEC_QKV + h * DEC_HD;
 
-    /* k and kd rows: DynamicTanh with the k-norm, then RoPE (pairs d, d + 16, d < 16) */
-    for (int i = tid; i < 2 * DEC_S * DEC_HD; i += 128) {
-        const int p = i / (DEC_S * DEC_HD), r = (i / DEC_HD) % DEC_S, d = i % DEC_HD;
-        const float x = base[(size_t)r * DEC_QKV + (p ? 3072 : 768) + d];
-        sk[p][r][d] = tanhf(a.ka * x) * a.kg[d] + a.kb[d];
+    /* this lane's 16 dims (16 lq ..) of q (or qd) and k (or kd) rows 16 b + lr, normalised
+     * and rotated */
+    float qf[3][16], kf[3][16];
+    {
+        const int qo = wave ? 2304 : 0, ko = wave ? 3072 : 768;
+        float qg[16], qb[16], kg[16], kb[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            qg[j] = a.qg[lq * 16 + j]; qb[j] = a.qb[lq * 16 + j];
+            kg[j] = a.kg[lq * 16 + j]; kb[j] = a.kb[lq * 16 + j];
+        }
+#pragma unroll
+        for (int b = 0; b < 3; b++) {
+            const int r = b * 16 + lr;
+            const bool ok = r < DEC_S;
+            const float *row = base + (size_t)(ok ? r : 0) * DEC_QKV + lq * 16;
+#pragma unroll
+            for (int j4 = 0; j4 < 4; j4++) {
+                const float4 x = *reinterpret_cast<const float4 *>(row + qo + 4 * j4);
+                const float4 y = *reinterpret_cast<const float4 *>(row + ko + 4 * j4);
+                qf[b][4 * j4 + 0] = x.x; qf[b][4 * j4 + 1] = x.y; qf[b][4 * j4 + 2] = x.z; qf[b][4 * j4 + 3] = x.w;
+                kf[b][4 * j4 + 0] = y.x; kf[b][4 * j4 + 1] = y.y; kf[b][4 * j4 + 2] = y.z; kf[b][4 * j4 + 3] = y.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                qf[b][j] = ok ? tanh_fast(a.qa * qf[b][j]) * qg[j] + qb[j] : 0.0f;
+                kf[b][j] = ok ? tanh_fast(a.ka * kf[b][j]) * kg[j] + kb[j] : 0.0f;
+            }
+            /* RoPE on dims 0..31: lanes lq = 0 hold d < 16, lq = 1 hold d + 16 */
+            const int rc = ok ? r : 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const float pq = __shfl_xor(qf[b][j], 16), pk = __shfl_xor(kf[b][j], 16);
+                if (lq < 2) {
+                    const float c = a.rcos[rc * DEC_RH + j], sn = a.rsin[rc * DEC_RH + j];
+                    if (lq == 0) {
+                        const float q0 = qf[b][j] * c, q1 = pq * sn, k0 = kf[b][j] * c, k1 = pk * sn;
+                        qf[b][j] = ok ? q0 - q1 : 0.0f;
+                        kf[b][j] = ok ? k0 - k1 : 0.0f;
+                    } else {
+                        const float q0 = qf[b][j] * c, q1 = pq * sn, k0 = kf[b][j] * c, k1 = pk * sn;
+                        qf[b][j] = ok ? q0 + q1 : 0.0f;
+                        kf[b][j] = ok ? k0 + k1 : 0.0f;
+                    }
+                }
+            }
+        }
     }
-    for (int i = tid; i < DEC_S * DEC_HD; i += 128) {
-        const int r = i / DEC_HD, d = i % DEC_HD;
-        sv[r][d] = base[(size_t)r * DEC_QKV + 1536 + d];
-    }
-    __syncthreads();
-    for (int i = tid; i < 2 * DEC_S * DEC_RH; i += 128) {
-        const int p = i / (DEC_S * DEC_RH), r = (i / DEC_RH) % DEC_S, d = i % DEC_RH;
-        const float x0 = sk[p][r][d], x1 = sk[p][r][d + DEC_RH];
-        const float c = a.rcos[r * DEC_RH + d], s = a.rsin[r * DEC_RH + d];
-        const float ac = x0 * c, bs = x1 * s, bc = x1 * c, as = x0 * s;
-        sk[p][r][d] = ac - bs;
-        sk[p][r][d + DEC_RH] = bc + as;
-    }
-    __syncthreads();
 
-    const int r = lane;
-    float o[DEC_HD];
-    if (r < DEC_S) {
-        /* this lane's query row (pair `wave`), normalised and rotated in registers */
-        float q[DEC_HD];
-        const float *qr = base + (size_t)r * DEC_QKV + (wave ? 2304 : 0);
+    /* S = q k^T */
+    f32x4_dec sc[3][3];
 #pragma unroll
-        for (int d = 0; d < DEC_HD; d++) q[d] = tanhf(a.qa * qr[d]) * a.qg[d] + a.qb[d];
+    for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int d = 0; d < DEC_RH; d++) {
-            const float c = a.rcos[r * DEC_RH + d], s = a.rsin[r * DEC_RH + d];
-            const float x0 = q[d], x1 = q[d + DEC_RH];
-            const float ac = x0 * c, bs = x1 * s, bc = x1 * c, as = x0 * s;
-            q[d] = ac - bs;
-            q[d + DEC_RH] = bc + as;
+        for (int j = 0; j < 3; j++) sc[i][j] = f32x4_dec{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < 16; st++)
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++)
+                sc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[i][st], kf[j][st], sc[i][j], 0, 0, 0);
+
+    /* softmax of each row over keys < 34 (block 2 holds keys 32 + lr) */
+    float *P = Ps[wave];
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            float x0 = sc[i][0][v] * 0.125f, x1 = sc[i][1][v] * 0.125f;
+            float x2 = lr < DEC_S - 32 ? sc[i][2][v] * 0.125f : -INFINITY;
+            float mx = fmaxf(fmaxf(x0, x1), x2);
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            x0 = exp_fast(x0 - mx); x1 = exp_fast(x1 - mx); x2 = exp_fast(x2 - mx);
+            float sum = (x0 + x1) + x2;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o);
+            const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+            const int row = i * 16 + 4 * lq + v;
+            P[row * DA_PS + lr] = x0 * inv;
+            P[row * DA_PS + 16 + lr] = x1 * inv;
+            P[row * DA_PS + 32 + lr] = x2 * inv;
         }
-        float sc[DEC_S];
-        float mx = -INFINITY;
+
+    /* O = P v over keys 12 lq + s (keys >= 34 have P = 0 and read no v) */
+    f32x4_dec oc[3][4];
 #pragma unroll
-        for (int j = 0; j < DEC_S; j++) {
-            float acc = 0.0f;
+    for (int i = 0; i < 3; i++)
 #pragma unroll
-            for (int d = 0; d < DEC_HD; d++) acc = __builtin_fmaf(q[d], sk[wave][j][d], acc);
-            sc[j] = acc * 0.125f;   /* 1 / sqrt(64) */
-            mx = fmaxf(mx, sc[j]);
+        for (int j = 0; j < 4; j++) oc[i][j] = f32x4_dec{0.0f, 0.0f, 0.0f, 0.0f};
+    {
+        float vf[4][12];
+#pragma unroll
+        for (int s2 = 0; s2 < 12; s2++) {
+            const int key = lq * 12 + s2;
+            const float *vr = base + (size_t)(key < DEC_S ? key : 0) * DEC_QKV + 1536 + lr;
+#pragma unroll
+            for (int j = 0; j < 4; j++) vf[j][s2] = key < DEC_S ? vr[16 * j] : 0.0f;
         }
-        float sum = 0.0f;
+        float pf[3][12];
 #pragma unroll
-        for (int j = 0; j < DEC_S; j++) {
-            sc[j] = exp_fast(sc[j] - mx);
-            sum += sc[j];
-        }
-        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int d = 0; d < DEC_HD; d++) o[d] = 0.0f;
+            for (int c4 = 0; c4 < 3; c4++) {
+                const float4 p4 = *reinterpret_cast<const float4 *>(&P[(i * 16 + lr) * DA_PS + lq * 12 + 4 * c4]);
+                pf[i][4 * c4 + 0] = p4.x; pf[i][4 * c4 + 1] = p4.y; pf[i][4 * c4 + 2] = p4.z; pf[i][4 * c4 + 3] = p4.w;
+            }
 #pragma unroll
-        for (int j = 0; j < DEC_S; j++) {
-            const float p = sc[j] * inv;
+        for (int s2 = 0; s2 < 12; s2++)
 #pragma unroll
-            for (int d = 0; d < DEC_HD; d++) o[d] = __builtin_fmaf(p, sv[j][d], o[d]);
-        }
-        if (wave == 1) {
+            for (int i = 0; i < 3; i++)
 #pragma unroll
-            for (int d = 0; d < DEC_HD; d++) sod[r][d] = o[d];
-        }
+                for (int j = 0; j < 4; j++)
+                    oc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pf[i][s2], vf[j][s2], oc[i][j], 0, 0, 0);
+    }
+
+    if (wave == 1) {
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) Os[((i * 4 + j) * 4 + v) * 64 + lane] = oc[i][j][v];
     }
     __syncthreads();
-    if (wave == 0 && r < DEC_S) {
-        uint32_t *dst = reinterpret_cast<uint32_t *>(a.merged + ((size_t)ch * DEC_S + r) * DEC_D + h * DEC_HD);
+    if (wave == 0) {
+        uint16_t *dst = a.merged + (size_t)ch * DEC_S * DEC_D + h * DEC_HD + lr;
 #pragma unroll
-        for (int d = 0; d < DEC_HD; d += 2)
-            dst[d >> 1] = (uint32_t)f2h_bits(o[d] - sod[r][d]) | ((uint32_t)f2h_bits(o[d + 1] - sod[r][d + 1]) << 16);
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int row = i * 16 + 4 * lq + v;
+                if (row < DEC_S) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        dst[(size_t)row * DEC_D + 16 * j] = f2h_bits(oc[i][j][v] - Os[((i * 4 + j) * 4 + v) * 64 + lane]);
+                }
+            }
     }
 }
 
@@ -181,12 +262,124 @@ __global__ __launch_bounds__(256) void k_dec_im2col(float *xc, const float *seq,
     }
 }
 
-/* audio[c][l * 256 + i] = mapped[l][c * 256 + i], l < Lt (src/aria_sa3_dec.c:108-116, 41-46) */
-__global__ __launch_bounds__(256) void k_dec_out(float4 *audio, const float4 *mapped, int Lt) {
-    const size_t n = (size_t)Lt * 128;   /* float4 per channel pair row: 512 / 4 */
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        const int l = (int)(i / 128), q = (int)(i % 128), c = q / 64, j = q % 64;
-        audio[(size_t)c * Lt * 64 + (size_t)l * 64 + j] = mapped[i];
+/* ---- the mapping convolution as an fp32 GEMM on the fp32 MFMA, unpatch fused ----
+ * audio[n / 256][m * 256 + n % 256] = sum_k xc[m][k] W[n][k] + b[n], m < M = T * 16, n < 512,
+ * k < 2304 (src/aria_sa3_dec.c:100-116: the mapping GEMM, the trim and aria_unpatch_stereo).
+ * v_mfma_f32_32x32x2_f32 keeps fp32 operands, as the reference keeps this GEMM in fp32.
+ * 256 threads = 2 x 2 waves, each owning FM x FN blocks of 32 x 32 (tile 64 FM rows of xc by
+ * 64 FN rows of W); k moves through LDS 32 at a time, double-buffered (one barrier per
+ * slice), the next slice's global loads in flight during the current slice's MFMAs. The
+ * MFMA computes W xc^T, so a lane's accumulators hold 4 consecutive n of one m: 4
+ * consecutive audio samples, one 16-byte store. Lane l of an MFMA supplies row l % 32 at
+ * k = 16 (l / 32) + j of the slice, j = 0..15 (any fixed k order gives the dot product),
+ * so each lane reads 16 consecutive floats of its row: four 16-byte LDS reads. Rows past
+ * M re-read row M - 1 and are not stored. */
+#define MAP_K 2304
+#define MAP_N 512
+#define MAP_KT 32
+#define MAP_SA 36          /* LDS row stride (floats): 16-byte reads of 16 rows hit 64 distinct banks */
+
+typedef float f32x16_dec __attribute__((ext_vector_type(16)));
+
+template <int FM, int FN>
+__global__ __launch_bounds__(256) void k_dec_map(float *audio, const float *xc, const float *W, const float *bias, int M) {
+    constexpr int BM = 64 * FM, BN = 64 * FN;
+    constexpr int LA = BM * MAP_KT / 4 / 256, LW = BN * MAP_KT / 4 / 256;   /* float4 loads per thread */
+    __shared__ __attribute__((aligned(16))) float As[2][BM * MAP_SA];
+    __shared__ __attribute__((aligned(16))) float Ws[2][BN * MAP_SA];
+    const int ntile = MAP_N / BN;
+    const int m0 = (blockIdx.x / ntile) * BM, n0 = (blockIdx.x % ntile) * BN;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+
+    f32x16_dec acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            float4 xa[FM], wa[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+                xa[i] = *reinterpret_cast<const float4 *>(&As[buf][(wm * 32 * FM + i * 32 + lr) * MAP_SA + lh * 16 + q4 * 4]);
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+                wa[j] = *reinterpret_cast<const float4 *>(&Ws[buf][(wn * 32 * FN + j * 32 + lr) * MAP_SA + lh * 16 + q4 * 4]);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(wa[j][e], xa[i][e], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    /* per thread: float4 q = tid + 256 i of the slice, row q / 8, column 4 (q % 8) */
+    const float *ga[LA], *gw[LW];
+#pragma unroll
+    for (int i = 0; i < LA; i++) {
+        const int q = tid + i * 256;
+        ga[i] = xc + (size_t)min(m0 + (q >> 3), M - 1) * MAP_K + (q & 7) * 4;
+    }
+#pragma unroll
+    for (int i = 0; i < LW; i++) {
+        const int q = tid + i * 256;
+        gw[i] = W + (size_t)(n0 + (q >> 3)) * MAP_K + (q & 7) * 4;
+    }
+    const int so = (tid >> 3) * MAP_SA + (tid & 7) * 4;   /* + 32 rows per i */
+    float4 ra[LA], rw[LW];
+#pragma unroll
+    for (int i = 0; i < LA; i++) ra[i] = *reinterpret_cast<const float4 *>(ga[i]);
+#pragma unroll
+    for (int i = 0; i < LW; i++) rw[i] = *reinterpret_cast<const float4 *>(gw[i]);
+#pragma unroll
+    for (int i = 0; i < LA; i++) *reinterpret_cast<float4 *>(&As[0][so + i * 32 * MAP_SA]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < LW; i++) *reinterpret_cast<float4 *>(&Ws[0][so + i * 32 * MAP_SA]) = rw[i];
+    __syncthreads();
+    constexpr int NK = MAP_K / MAP_KT;
+    for (int kt = 0; kt < NK; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < NK) {
+#pragma unroll
+            for (int i = 0; i < LA; i++) ra[i] = *reinterpret_cast<const float4 *>(ga[i] + (kt + 1) * MAP_KT);
+#pragma unroll
+            for (int i = 0; i < LW; i++) rw[i] = *reinterpret_cast<const float4 *>(gw[i] + (kt + 1) * MAP_KT);
+        }
+        compute(cur);
+        if (kt + 1 < NK) {
+#pragma unroll
+            for (int i = 0; i < LA; i++) *reinterpret_cast<float4 *>(&As[cur ^ 1][so + i * 32 * MAP_SA]) = ra[i];
+#pragma unroll
+            for (int i = 0; i < LW; i++) *reinterpret_cast<float4 *>(&Ws[cur ^ 1][so + i * 32 * MAP_SA]) = rw[i];
+        }
+        __syncthreads();
+    }
+
+    /* accumulator r of lane l: n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32 (per block) */
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+        const int m = m0 + wm * 32 * FM + i * 32 + lr;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int n = n0 + wn * 32 * FN + j * 32 + 8 * g + 4 * lh;
+                const float4 b = *reinterpret_cast<const float4 *>(bias + n);
+                float4 o;
+                o.x = acc[i][j][4 * g + 0] + b.x;
+                o.y = acc[i][j][4 * g + 1] + b.y;
+                o.z = acc[i][j][4 * g + 2] + b.z;
+                o.w = acc[i][j][4 * g + 3] + b.w;
+                *reinterpret_cast<float4 *>(audio + (size_t)(n >> 8) * M * 256 + (size_t)m * 256 + (n & 255)) = o;
+            }
     }
 }
 
@@ -220,15 +413,20 @@ extern "C" hipError_t aria_k_dec_attn(uint16_t *merged, const float *qkv, float 
     DecAttnArgs a;
     a.merged = merged; a.qkv = qkv; a.qg = qg; a.qb = qb; a.kg = kg; a.kb = kb; a.qa = qa; a.ka = ka;
     a.rcos = rcos; a.rsin = rsin;
-    hipLaunchKernelGGL(k_dec_attn, dim3(nch * 12), dim3(128), 0, s, a, 12);
+    hipLaunchKernelGGL(k_dec_attn_mfma, dim3(nch * 12), dim3(128), 0, s, a, 12);
     return hipGetLastError();
 }
 extern "C" hipError_t aria_k_dec_im2col(float *xc, const float *seq, int Lt, int Lout, hipStream_t s) {
     hipLaunchKernelGGL(k_dec_im2col, grid_for((size_t)Lt * 3 * DEC_D), dim3(256), 0, s, xc, seq, Lt, Lout);
     return hipGetLastError();
 }
-extern "C" hipError_t aria_k_dec_out(float *audio, const float *mapped, int Lt, hipStream_t s) {
-    hipLaunchKernelGGL(k_dec_out, grid_for((size_t)Lt * 128), dim3(256), 0, s, (float4 *)audio,
-                       (const float4 *)mapped, Lt);
+/* audio [2, M * 256] = unpatch(xc [M, 2304] . W [512, 2304]^T + b): 64 x 64 tiles while the
+ * 128 x 128 grid would leave CUs idle (M < 16384), else 128 x 128 */
+extern "C" hipError_t aria_k_dec_map(float *audio, const float *xc, const float *W, const float *b, int M,
+                                     hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    const int t128 = (M + 127) / 128 * (MAP_N / 128);
+    if (t128 >= 512) hipLaunchKernelGGL((k_dec_map<2, 2>), dim3(t128), dim3(256), 0, s, audio, xc, W, b, M);
+    else hipLaunchKernelGGL((k_dec_map<1, 1>), dim3((M + 63) / 64 * (MAP_N / 64)), dim3(256), 0, s, audio, xc, W, b, M);
     return hipGetLastError();
 }

@@ -399,6 +399,16 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
         launch_cfg<C2, WT, AF16>(a, s);
         return hipGetLastError();
     } else {
+    if constexpr (WT == ARIA_WF16) {
+        /* fp16 weights on the LDS-DMA kernel: explicit tiles 13.., or picked for N <= 1024
+         * (64 x 128 tiles, two per CU), where it measured 10-17 % faster than the LDS-operand
+         * kernel on the decoder's to_out / ff_out (M 1870 and 11016, K 768 and 2304); wider N
+         * stays on the LDS-operand kernel's 128 x 128 / 192 x 128 tiles */
+        if (tiles >= 13) return qgemm_big_launch(a, WT, tiles - 13, s);
+        if (tiles == 0 && a.N <= 1024 && a.K % 64 == 0 && (!a.gelu || a.epi.mode == ARIA_EPI_STORE) &&
+            a.epi.mode != ARIA_EPI_HEADS)
+            return qgemm_big_launch(a, WT, 0, s);
+    }
     if constexpr (WT != ARIA_WF16) {
         /* the LDS-DMA kernel (k_qgemm_big.hip): explicit tiles 13.. (configuration tiles - 13),
          * or picked for the shapes where it measured fastest: N <= 1024 without HEADS (96 x 128

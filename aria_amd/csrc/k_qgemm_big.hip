@@ -1,6 +1,7 @@
 /*
  * k_qgemm_big.hip - the large-tile dequant-on-use GEMM (gfx950 MFMA):
- * y[M,N] = x[M,K] W[N,K]^T (+ b) for Q8 / Q4 weights and fp16 activations, K % 64 == 0.
+ * y[M,N] = x[M,K] W[N,K]^T (+ b) for Q8 / Q4 / fp16 weights and fp16 activations (and the
+ * W8A8 int8 form), K % 64 == 0.
  * Replaces the same reference functions as k_qgemm.hip (aria_linear_q8 / aria_linear_q4,
  * src/aria_quant.c:98-145, 469-538; the reference's device form dequantizes into an fp16
  * scratch and calls cublasGemmEx, src/aria_cuda.cu:1009-1035). Shares the argument block,
@@ -112,6 +113,7 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t m0) {
  *   [0, 128 BM)            activations [BM][64] fp16 (W8A8: [BM][128] int8), chunk-swizzled (xo)
  *   Q8: [.., + 64 BN)      weights [BN][64] int8; 16 B chunk c of row r at c ^ ((r >> 2) & 3)
  *   W8A8: [.., + 128 BN)   weights [BN][128] int8, chunk-swizzled as the activations
+ *   fp16: [.., + 128 BN)   weights [BN][64] fp16, chunk-swizzled as the activations
  *   Q4: [.., + 32 BN)      nibbles [BN][32 B]
  *       [.., + 4096)       [min, step] pairs of the K-tile, 16 B per row: wave w's 64 slots
  *                          at 1024 w (FN = 1: rows 32w.. in slots 0-31, 32-63 repeat them) */
@@ -119,11 +121,11 @@ template <int WT, int FM, int FN>
 struct Stage {
     static constexpr int BM = 32 * FM, BN = 128 * FN;
     static constexpr int A = BM * 128;
-    static constexpr int WQ = WT == ARIA_WI8 ? BN * 128 : WT == ARIA_WQ8 ? BN * 64 : BN * 32;
+    static constexpr int WQ = (WT == ARIA_WI8 || WT == ARIA_WF16) ? BN * 128 : WT == ARIA_WQ8 ? BN * 64 : BN * 32;
     static constexpr int WS = WT == ARIA_WQ4 ? 4096 : 0;
     static constexpr int BYTES = A + WQ + WS;
     /* VMEM instructions one wave issues per K-tile */
-    static constexpr int DMA = FM + (WT == ARIA_WI8 ? 4 * FN : WT == ARIA_WQ8 ? 2 * FN : FN + 1);
+    static constexpr int DMA = FM + ((WT == ARIA_WI8 || WT == ARIA_WF16) ? 4 * FN : WT == ARIA_WQ8 ? 2 * FN : FN + 1);
     /* k per K-tile: 64 fp16 activations, or 128 int8 ones (W8A8), in the 128-byte rows */
     static constexpr int KK = WT == ARIA_WI8 ? 128 : 64;
 };
@@ -154,7 +156,7 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
     uint32_t magic = 0x64006400u;           /* fp16 1024 in both halves, kept in a VGPR */
     asm volatile("" : "+v"(magic));
     const uint32_t sbase = (uint32_t)(uintptr_t)smem;
-    constexpr int NWQ = WT == ARIA_WI8 ? 4 * FN : WT == ARIA_WQ8 ? 2 * FN : FN;   /* weight DMA per wave */
+    constexpr int NWQ = (WT == ARIA_WI8 || WT == ARIA_WF16) ? 4 * FN : WT == ARIA_WQ8 ? 2 * FN : FN;   /* weight DMA per wave */
     const int rbase = wave * 32 * FN;                    /* this wave's first weight row */
 
     /* per-lane global sources of this wave's DMA slots for K-tile 0 of tile (m0, n0);
@@ -175,9 +177,9 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
 #pragma unroll
         for (int i = 0; i < NWQ; i++) {
             const int p = 64 * i + lane;
-            if constexpr (WT == ARIA_WI8) {
+            if constexpr (WT == ARIA_WI8 || WT == ARIA_WF16) {   /* 128-byte rows per K-tile */
                 const int r = rbase + (p >> 3), c = (p & 7) ^ ((r >> 1) & 7);
-                wsrc[i] = (const uint8_t *)a.q + (size_t)min(n0 + r, a.N - 1) * a.K + 16 * c;
+                wsrc[i] = (const uint8_t *)a.q + (size_t)min(n0 + r, a.N - 1) * a.K * (WT == ARIA_WF16 ? 2 : 1) + 16 * c;
             } else if constexpr (WT == ARIA_WQ8) {
                 const int r = rbase + (p >> 2), c = (p & 3) ^ ((r >> 2) & 3);
                 wsrc[i] = (const uint8_t *)a.q + (size_t)min(n0 + r, a.N - 1) * a.K + 16 * c;
@@ -207,7 +209,10 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
             }
 #pragma unroll
             for (int i = 0; i < FM; i++) dma16(xsrc[i] + k64 * KB, st + (256 * i + 64 * wave) * 16);
-            if constexpr (WT == ARIA_WQ8) {
+            if constexpr (WT == ARIA_WF16) {
+#pragma unroll
+                for (int i = 0; i < NWQ; i++) dma16(wsrc[i] + k64 * 128, st + St::A + rbase * 128 + 1024 * i);
+            } else if constexpr (WT == ARIA_WQ8) {
 #pragma unroll
                 for (int i = 0; i < NWQ; i++) dma16(wsrc[i] + k64 * KB, st + St::A + rbase * 64 + 1024 * i);
             } else {
@@ -252,6 +257,26 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
             return;
         }
         const uint16_t *X = reinterpret_cast<const uint16_t *>(S);
+        if constexpr (WT == ARIA_WF16) {
+            /* fp16 weights: both operands straight from LDS, the same k order as the
+             * activation fragments of the packed paths */
+            const uint16_t *Wr = reinterpret_cast<const uint16_t *>(S + St::A);
+            static_for<4>([&](auto KS) __attribute__((always_inline)) {
+                constexpr int ks = decltype(KS)::value;
+                half8_t xf[FM], wf[FN];
+#pragma unroll
+                for (int i = 0; i < FM; i++) xf[i] = *reinterpret_cast<const half8_t *>(&X[xo(i * 32 + lrow, 4 * lh + ks)]);
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    wf[j] = *reinterpret_cast<const half8_t *>(&Wr[xo(rbase + 32 * j + lrow, 4 * lh + ks)]);
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[i][j], 0, 0, 0);
+            });
+            return;
+        } else {
         WSt<WT, FN> ws;
 #pragma unroll
         for (int j = 0; j < FN; j++) {
@@ -299,13 +324,19 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
                 for (int j = 0; j < FN; j++) wa[j] = wn[j];
             }
         });
+        }
         });
     };
 
     /* workgroup barrier without a memory fence: the loop's only LDS writes are the DMA
-     * transfers, whose completion each wave has waited for on vmcnt just before */
+     * transfers, whose completion each wave has waited for on vmcnt just before. Every LDS
+     * read of the step must have returned before the barrier (lgkmcnt(0)): the compiler
+     * places the last fragment reads' waits next to their MFMAs, which it may schedule
+     * past the barrier, and a read still in flight there races with the next step's DMA
+     * into the same stage (seen as one 32 x 32 block with a wrong k-slice). */
     auto barrier = []() __attribute__((always_inline)) {
         asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0xC07F);   /* lgkmcnt(0); vmcnt and expcnt left at their maxima */
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     };
@@ -391,10 +422,31 @@ static const int big_fm[] = {3, 4, 4};
 static const int big_fn[] = {1, 2, 1};
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
+
+/* fp16 weights (the decoder's GEMMs): 128-byte weight rows per K-tile, twice the Q8 bytes, so
+ * the tiles are those that fit three stages: index = cfg
+ *   0: 64 x 128, two workgroups per CU    1: 64 x 256    2: 128 x 256    3: 128 x 128 */
+#define BIG_F16_CFGS(X) X(0, 2, 1, 2) X(1, 2, 2, 1) X(2, 4, 2, 1) X(3, 4, 1, 1)
+static const int big_f16_fn[] = {1, 2, 2, 1};
+
+static hipError_t qgemm_big_f16_launch(const QArgs &a, int cfg, hipStream_t s) {
+    if (cfg < 0 || cfg >= (int)(sizeof big_f16_fn / sizeof big_f16_fn[0]) ||
+        (a.epi.mode == ARIA_EPI_HEADS && big_f16_fn[cfg] < 2))
+        return hipErrorInvalidValue;
+#define F16_CASE(i, fm, fn, mb) \
+    case i: launch_big<ARIA_WF16, fm, fn, mb>(a, s); break;
+    switch (cfg) {
+        BIG_F16_CFGS(F16_CASE)
+        default: return hipErrorInvalidValue;
+    }
+#undef F16_CASE
+    return hipGetLastError();
+}
 int qgemm_big_bm(int cfg) { return 32 * big_fm[cfg]; }
 int qgemm_big_bn(int cfg) { return 128 * big_fn[cfg]; }
 
 hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
+    if (wt == ARIA_WF16 && a.K % KB == 0 && (!a.gelu || a.epi.mode == ARIA_EPI_STORE)) return qgemm_big_f16_launch(a, cfg, s);
     if (a.K % KB || cfg < 0 || cfg >= qgemm_big_ncfg() || (a.gelu && a.epi.mode != ARIA_EPI_STORE) ||
         (a.epi.mode == ARIA_EPI_HEADS && big_fn[cfg] < 2))
         return hipErrorInvalidValue;

@@ -134,3 +134,68 @@ def test_qgemm_every_tile_shape(hip, port, tiles, wtype):
         hip.check(L.aria_hip_qlinear_ex_dev(dy.p, 0, dx.p, xf16, wtype, dq.p, ds.p, db.p, M, K, N, tiles, None))
         sync()
         assert relerr_max(dy.to_host(), want) <= GATE, (tiles, wtype, xf16)
+
+
+@pytest.mark.parametrize("tiles", [13, 14, 15, 16])
+@pytest.mark.parametrize("wtype", [0, 1, 2])
+def test_qgemm_lds_dma_tiles(hip, port, tiles, wtype):
+    """The LDS-DMA kernel's tile configurations (tiles 13.. = configuration tiles - 13; Q8/Q4
+    have three, fp16 weights four) with ragged M and N edges, fp16 activations; fp16 weights
+    against the float64 product of the same fp16 values."""
+    from aria_amd.device import DeviceArray, sync
+    if wtype != 2 and tiles == 16:
+        pytest.skip("Q8/Q4 compile three LDS-DMA configurations")
+    r = rng(140 + tiles * 3 + wtype)
+    M, K, N = 197, 384, 136
+    x = randn(r, (M, K)).astype(np.float16); W = randn(r, (N, K), 0.05); b = randn(r, N, 0.02)
+    if wtype == 2:
+        q, s = W.astype(np.float16), None
+        want = (x.astype(np.float64) @ q.astype(np.float64).T + b).astype(np.float32)
+    else:
+        q, s = port.q8_quant(W) if wtype == 0 else port.q4_quant(W)
+        xr = x.astype(np.float32)
+        want = port.linear_q8(xr, q, s, b) if wtype == 0 else port.linear_q4(xr, q, s, b)
+    L = hip.lib()
+    dx, dq, db = (DeviceArray.from_host(a) for a in (x, q, b))
+    ds = DeviceArray.from_host(s) if s is not None else None
+    dy = DeviceArray((M, N), np.float32)
+    hip.check(L.aria_hip_qlinear_ex_dev(dy.p, 0, dx.p, 1, wtype, dq.p, ds.p if ds else None, db.p, M, K, N,
+                                        tiles, None))
+    sync()
+    assert relerr_max(dy.to_host(), want) <= GATE, (tiles, wtype)
+
+
+@pytest.mark.parametrize("wtype,tiles,MKN", [(2, 13, (5000, 768, 4608)), (0, 13, (2592, 1024, 1024)),
+                                             (1, 15, (2592, 1024, 3072))])
+def test_qgemm_lds_dma_repeatable(hip, port, wtype, tiles, MKN):
+    """Repeated launches of the LDS-DMA kernel on the same inputs give the same bits. Its
+    pipeline overwrites a stage by DMA one step after the stage was read, so an LDS read still
+    in flight at the step's barrier would let the next DMA change a fragment under it: seen as
+    one 32 x 32 block wrong in about one launch in four at the first shape before every
+    fragment read was waited for ahead of the barrier."""
+    from aria_amd.device import DeviceArray, sync
+    M, K, N = MKN
+    r = rng(170 + wtype)
+    x = randn(r, (M, K)).astype(np.float16); W = randn(r, (N, K), 1.0 / np.sqrt(K))
+    if wtype == 2:
+        q, s = W.astype(np.float16), None
+    else:
+        q, s = port.q8_quant(W) if wtype == 0 else port.q4_quant(W)
+    L = hip.lib()
+    dx, dq = DeviceArray.from_host(x), DeviceArray.from_host(q)
+    ds = DeviceArray.from_host(s) if s is not None else None
+    dy = DeviceArray((M, N), np.float32)
+    first = None
+    for rep in range(6):
+        hip.check(L.aria_hip_qlinear_ex_dev(dy.p, 0, dx.p, 1, wtype, dq.p, ds.p if ds else None, None, M, K, N,
+                                            tiles, None))
+        sync()
+        y = dy.to_host()
+        if first is None:
+            first = y
+            if wtype == 2:
+                rows = np.arange(0, M, 97)
+                want = x[rows].astype(np.float64) @ q.astype(np.float64).T
+                assert relerr_max(y[rows], want) <= GATE
+        else:
+            assert np.array_equal(y, first), (rep, int((y != first).sum()))
