@@ -8,20 +8,22 @@
  * the unpack and the fused epilogue with the other GEMM kernels (qgemm_dev.h).
  *
  * Workgroup: 4 waves share one activation tile of BM = 32 FM rows; wave w owns FN blocks
- * of 32 weight rows (BN = 128 FN per workgroup) and loads them straight from the packed
- * layout into registers in the MFMA operand layout. The cost that grows with the tile is
- * the unpack: each weight is unpacked once per workgroup and feeds BM rows, so unpack VALU
- * per MFMA falls as 1 / FM; the LDS bytes per MFMA fall as 1 / FN (FN = 2: 0.5 KB per
- * 32x32x16 MFMA, half the LDS rate at full MFMA rate). FM up to 8 keeps 32 FM FN
- * accumulator registers per lane (the AGPRs) and one wave per SIMD.
+ * of 32 weight rows (BN = 128 FN per workgroup). Both operands travel HBM -> LDS by LDS DMA
+ * (global_load_lds_dwordx4: no staging registers, no VALU): the activation tile is spread over
+ * all four waves' transfers and read by all of them; wave w moves its own weight rows and reads
+ * them back in the MFMA operand layout (Q8 / Q4 unpacked in registers, fp16 and int8 used as
+ * they are). The cost that grows with the tile is the unpack: each weight is unpacked once per
+ * workgroup and feeds BM rows, so unpack VALU per MFMA falls as 1 / FM.
  *
- * Pipeline, K-tile 64, three stages: the activation tile of K-tile t arrives in LDS by
- * LDS DMA (global_load_lds_dwordx4, no staging registers) two K-tiles before it is
- * multiplied, into LDS buffer t % 3; the weights of K-tile t arrive in register stage
- * t % 3, also two K-tiles ahead. Step t: issue the loads of t + 2, multiply t, wait for
- * the loads of t + 1 (issued one whole step earlier), one barrier. The three buffers are
- * separate LDS objects picked by compile-time indices, so the compiler can see that the
- * fragment reads of buffer t never touch the pending DMA of buffers t + 1, t + 2.
+ * Pipeline, K-tile 64 (128 for int8), NST = 3 stages: K-tile t lands in stage t % 3 two
+ * K-tiles before it is multiplied. Step t: issue the transfers of t + 2, multiply t, wait for
+ * this wave's transfers of t + 1 (vmcnt, the ones of t + 2 stay in flight), barrier. The
+ * barrier carries no memory fence (a fence would drain every transfer in flight) but waits
+ * for the step's LDS reads (lgkmcnt(0)): stage t % 3 is refilled by the transfers issued in
+ * step t + 1, so no fragment read of step t may still be in flight when any wave passes the
+ * barrier. Stage offsets are compile-time constants (the loop is unrolled by NST), and the
+ * transfers are inline assembly with a memory clobber, so the compiler neither waits for them
+ * nor moves fragment reads across them.
  *
  * Contraction order inside a K-tile (as in k_qgemm_wr.hip): lane half h = l / 32 covers
  * k in [32h, 32h + 32) and MFMA step ks its 8 k at 32h + 8ks, for both operands; a Q4
