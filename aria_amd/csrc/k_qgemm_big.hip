@@ -417,11 +417,14 @@ static void launch_big(const QArgs &a, hipStream_t s) {
 /* the configurations compiled (FM, FN, workgroups per CU), index = the cfg argument; measured
  * at M = 2592 (DiT shapes), fp16 activations:
  *   0: 96 x 128, two per CU: N <= 1024 (sa_out, ca_out, ff_out; K = 1024 and 4096)
- *   1: 128 x 256, one per CU: the qkv projection (HEADS, N = 3072)
- *   2: 128 x 128, two per CU: N = 3072 without HEADS */
-#define BIG_CFGS(X) X(0, 3, 1, 2) X(1, 4, 2, 1) X(2, 4, 1, 2)
-static const int big_fm[] = {3, 4, 4};
-static const int big_fn[] = {1, 2, 1};
+ *   1: 128 x 256, one per CU (explicit requests)
+ *   2: 128 x 128, two per CU: N = 3072 without HEADS
+ *   3: 64 x 256, two per CU: the HEADS projections (qkv N = 3072, ca_q N = 1024): a head's 64
+ *      columns in one wave, and the second workgroup per CU covers the other's HEADS epilogue
+ *      (block 214 -> 204 us against 128 x 256 for qkv and the weights-in-registers ca_q) */
+#define BIG_CFGS(X) X(0, 3, 1, 2) X(1, 4, 2, 1) X(2, 4, 1, 2) X(3, 2, 2, 2)
+static const int big_fm[] = {3, 4, 4, 2};
+static const int big_fn[] = {1, 2, 1, 2};
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
 

@@ -139,12 +139,10 @@ def test_qgemm_every_tile_shape(hip, port, tiles, wtype):
 @pytest.mark.parametrize("tiles", [13, 14, 15, 16])
 @pytest.mark.parametrize("wtype", [0, 1, 2])
 def test_qgemm_lds_dma_tiles(hip, port, tiles, wtype):
-    """The LDS-DMA kernel's tile configurations (tiles 13.. = configuration tiles - 13; Q8/Q4
-    have three, fp16 weights four) with ragged M and N edges, fp16 activations; fp16 weights
-    against the float64 product of the same fp16 values."""
+    """The LDS-DMA kernel's tile configurations (tiles 13.. = configuration tiles - 13; four
+    each for Q8/Q4 and for fp16 weights) with ragged M and N edges, fp16 activations; fp16
+    weights against the float64 product of the same fp16 values."""
     from aria_amd.device import DeviceArray, sync
-    if wtype != 2 and tiles == 16:
-        pytest.skip("Q8/Q4 compile three LDS-DMA configurations")
     r = rng(140 + tiles * 3 + wtype)
     M, K, N = 197, 384, 136
     x = randn(r, (M, K)).astype(np.float16); W = randn(r, (N, K), 0.05); b = randn(r, N, 0.02)
