@@ -68,6 +68,9 @@ def parse():
     ap.add_argument("--pmc-gemm", action="store_true",
                     help="for rocprofv3 --pmc: the config-3 GEMMs (5 launches each) and two forwards of each "
                          "config-4 block variant, untimed")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only the vendor-library reference points: PyTorch's fp16 GEMM (hipBLASLt) and "
+                         "scaled_dot_product_attention at this build's GEMM and attention shapes")
     return ap.parse_args()
 
 
@@ -263,6 +266,9 @@ def main():
     print(f"[bench] device: {aria_amd.device_info()}", file=sys.stderr, flush=True)
 
     rng = np.random.default_rng(SEED)
+    if args.vendor:
+        print(json.dumps({"vendor": vendor_leg()}), flush=True)
+        return
     if args.pmc_gemm:
         def run_only(fn, reps):
             for i in range(reps):
@@ -551,6 +557,46 @@ def block_leg(DeviceArray, time_loop, stream, rng, reps):
                      "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "flop": flop,
                      "weight_bytes": blk.weight_bytes}
         blk.free()
+    return out
+
+
+def vendor_leg(reps=50):
+    """What the vendor libraries reach on the same shapes, as a yardstick for the hand-written
+    kernels (not part of the product): torch.matmul in fp16 (hipBLASLt; plain fp16 weights, no
+    dequantization, fp16 output) at the config-3, DiT-block and decoder GEMM shapes, and
+    torch.nn.functional.scaled_dot_product_attention in fp16 at the block's self and cross
+    attention shapes. CUDA events around `reps` back-to-back calls after 5 warm-up calls."""
+    import torch
+    import torch.nn.functional as F
+    dev = "cuda"
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e3
+
+    out = {"device": torch.cuda.get_device_name(0), "torch": torch.__version__}
+    g = torch.Generator(device=dev).manual_seed(SEED)
+    for (M, K, N) in ((2592, 1024, 4096), (2592, 4096, 1024), (2592, 1024, 3072), (2592, 1024, 1024),
+                      (11016, 768, 3840), (11016, 768, 4608), (11016, 2304, 768)):
+        a = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
+        b = torch.randn(N, K, device=dev, dtype=torch.float16, generator=g)
+        us = timed(lambda: a @ b.t())
+        out[f"gemm_f16_M{M}_K{K}_N{N}"] = {"us": round(us, 1), "TFLOP/s": round(2.0 * M * N * K / us / 1e6, 1)}
+    for (Sq, Sk) in ((1296, 1296), (1296, 256)):
+        q = torch.randn(B, H, Sq, HD, device=dev, dtype=torch.float16, generator=g)
+        k = torch.randn(B, H, Sk, HD, device=dev, dtype=torch.float16, generator=g)
+        v = torch.randn(B, H, Sk, HD, device=dev, dtype=torch.float16, generator=g)
+        us = timed(lambda: F.scaled_dot_product_attention(q, k, v))
+        out[f"sdpa_f16_B{B}_H{H}_S{Sq}_Sk{Sk}"] = {"us": round(us, 1),
+                                                    "TFLOP/s": round(4.0 * B * H * Sq * Sk * HD / us / 1e6, 1)}
     return out
 
 
