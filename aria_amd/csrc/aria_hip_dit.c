@@ -525,7 +525,9 @@ enum { GRAPH_NONE = 0, GRAPH_LIVE = 1, GRAPH_OFF = 2 };
 struct aria_cuda_dit {
     int depth, ed, H, inner, io_ch, n_mem, rot;
     aria_hip_dit_block **blk;
-    float *pre, *post, *pin, *pout, *mem;   /* fp32: [C,C], [C,C], [ed,C], [C,ed], [n_mem, ed] */
+    uint16_t *pre, *post, *pin, *pout;      /* fp16: [C,C], [C,C], [ed,C], [C,ed] (as the reference's
+                                             * device step keeps them, src/aria_cuda.cu:1197-1200) */
+    float *mem;                             /* fp32 [n_mem, ed] */
     hipStream_t st;
     /* request state */
     int have_req, B, T, S, Sc, cur_step;
@@ -554,6 +556,22 @@ static int up_mat(float **d, const float *h, size_t n) {
     *d = NULL;
     if (!h) return 0;
     return upv(d, h, n, NULL);
+}
+
+/* fp16 device copy of an fp32 host matrix (NULL stays NULL), converted on the device (RTNE) */
+static int up_mat16(uint16_t **d, const float *h, size_t n, hipStream_t s) {
+    *d = NULL;
+    if (!h) return 0;
+    float *tmp = NULL;
+    int rc = upv(&tmp, h, n, NULL);
+    if (!rc) rc = dalloc((void **)d, n * 2, NULL);
+    if (!rc) {
+        hipError_t e = aria_k_f32_to_f16(*d, tmp, n, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = FAIL(e, "fp16 conversion (io projections)");
+    }
+    dfree(tmp);
+    return rc;
 }
 
 /* forget the captured step (buffers or weights it names are about to change); the next
@@ -587,7 +605,7 @@ void aria_cuda_dit_free(aria_cuda_dit *h) {
     req_free(h);
     if (h->blk) for (int b = 0; b < h->depth; b++) aria_hip_dit_block_free(h->blk[b]);
     free(h->blk);
-    float *w[] = {h->pre, h->post, h->pin, h->pout, h->mem};
+    void *w[] = {h->pre, h->post, h->pin, h->pout, h->mem};
     for (size_t i = 0; i < sizeof w / sizeof *w; i++) dfree(w[i]);
     if (h->up) hipStreamSynchronize(h->up);
     sbuf_release(&h->gc_tab, 0);
@@ -639,10 +657,10 @@ aria_cuda_dit *aria_hip_dit_create_ex(const aria_sa3_dit_view *v, aria_dtype pre
         if (!h->blk[b]) rc = ARIA_HIP_EINVAL;
     }
     const size_t C = (size_t)v->io_ch, E = (size_t)v->ed;
-    if (!rc) rc = up_mat(&h->pre, v->preprocess, C * C);
-    if (!rc) rc = up_mat(&h->post, v->postprocess, C * C);
-    if (!rc) rc = up_mat(&h->pin, v->project_in, E * C);
-    if (!rc) rc = up_mat(&h->pout, v->project_out, C * E);
+    if (!rc) rc = up_mat16(&h->pre, v->preprocess, C * C, h->st);
+    if (!rc) rc = up_mat16(&h->post, v->postprocess, C * C, h->st);
+    if (!rc) rc = up_mat16(&h->pin, v->project_in, E * C, h->st);
+    if (!rc) rc = up_mat16(&h->pout, v->project_out, C * E, h->st);
     if (!rc && v->n_mem) rc = up_mat(&h->mem, v->memory_tokens, (size_t)v->n_mem * E);
     if (!rc && (!h->pin || !h->pout)) rc = ARIA_HIP_EINVAL;
     if (rc) {
@@ -786,30 +804,51 @@ void aria_cuda_dit_set_step(aria_cuda_dit *h, int step) {
 /* one velocity evaluation on the handle's buffers (src/aria_sa3_dit.c:734-777):
  * [C,T] -> [T,C]; xtc += preprocess(xtc); seq = [memory tokens | project_in(xtc)];
  * depth blocks; out = project_out(seq[n_mem:]); out += postprocess(out); -> [C,T] */
+/* y [M, N] (+)= x [M, K] . W^T with fp32 x rounded to fp16 in the GEMM's staging and fp16 W,
+ * fp32 accumulation and output: the reference's device step runs its four io projections so
+ * (gemm_f16w, src/aria_cuda.cu:906-917). add: y += the product (the residual of the pre/post
+ * convolutions, x == y), in the epilogue when the MFMA kernel takes the shape and one 128-wide
+ * tile covers N (fp32 activations run 128 x 128 tiles), so each workgroup owns whole rows and has
+ * read them before it writes them; otherwise through dtmp and k_add. */
+static int io_gemm(aria_cuda_dit *h, float *y, const float *x, const uint16_t *W, int M, int K, int N, int add,
+                   hipStream_t s) {
+    const int mfma = K % 32 == 0 && N % 4 == 0;
+    if (add && mfma && N <= 128) {
+        aria_qgemm_epi e;
+        memset(&e, 0, sizeof e);
+        e.mode = ARIA_EPI_ADD;
+        e.rows_per_batch = M;
+        STEP(aria_k_qgemm_e(y, 0, x, 0, ARIA_WF16, W, NULL, NULL, M, K, N, 0, 0, &e, s), "k_qgemm (io projection)");
+        return 0;
+    }
+    float *dst = add ? h->dtmp : y;
+    STEP(aria_k_qgemm_e(dst, 0, x, 0, ARIA_WF16, W, NULL, NULL, M, K, N, 0, 0, NULL, s), "k_qgemm (io projection)");
+    if (add) STEP(aria_k_add(y, y, dst, (size_t)M * N, s), "k_add (io projection)");
+    return 0;
+}
+
 static int step_compute(aria_cuda_dit *h, hipStream_t s) {
     const int B = h->B, T = h->T, S = h->S, C = h->io_ch, E = h->ed, Mt = h->n_mem;
-    const size_t nxc = (size_t)B * T * C;
+    int rc;
     STEP(aria_k_transpose(h->dxtc, h->dx, C, T, B, s), "k_transpose (x)");
-    if (h->pre) {
-        STEP(aria_k_sgemm(h->dtmp, h->dxtc, h->pre, NULL, B * T, C, C, 1, 1.0f, 1, 0, 0, 0, s), "preprocess");
-        STEP(aria_k_add(h->dxtc, h->dxtc, h->dtmp, nxc, s), "k_add (preprocess)");
-    }
+    if (h->pre && (rc = io_gemm(h, h->dxtc, h->dxtc, h->pre, B * T, C, C, 1, s))) return rc;
     for (int b = 0; b < B && Mt; b++)
         STEP(hipMemcpyAsync(h->dseq + (size_t)b * S * E, h->mem, (size_t)Mt * E * 4, hipMemcpyDeviceToDevice, s),
              "memory tokens");
-    STEP(aria_k_sgemm(h->dseq + (size_t)Mt * E, h->dxtc, h->pin, NULL, T, E, C, 1, 1.0f, B, (long long)T * C, 0,
-                      (long long)S * E, s), "project_in");
+    /* project_in / project_out: one GEMM over both sequences when no memory tokens interleave */
+    const int nb = Mt ? B : 1, rows = Mt ? T : B * T;
+    for (int b = 0; b < nb; b++)
+        if ((rc = io_gemm(h, h->dseq + ((size_t)b * S + Mt) * E, h->dxtc + (size_t)b * T * C, h->pin, rows, C, E, 0, s)))
+            return rc;
     for (int b = 0; b < h->depth; b++) {
-        int rc = block_forward(h->blk[b], h->dseq, B, S, h->dgcond, h->ck[b], h->cv[b], h->Sc, h->cos_t, h->sin_t,
-                               h->rot, h->local ? h->local[b] : NULL, h->ws, h->ws_bytes, s);
+        rc = block_forward(h->blk[b], h->dseq, B, S, h->dgcond, h->ck[b], h->cv[b], h->Sc, h->cos_t, h->sin_t,
+                           h->rot, h->local ? h->local[b] : NULL, h->ws, h->ws_bytes, s);
         if (rc) return rc;
     }
-    STEP(aria_k_sgemm(h->dout, h->dseq + (size_t)Mt * E, h->pout, NULL, T, C, E, 1, 1.0f, B, (long long)S * E, 0,
-                      (long long)T * C, s), "project_out");
-    if (h->post) {
-        STEP(aria_k_sgemm(h->dtmp, h->dout, h->post, NULL, B * T, C, C, 1, 1.0f, 1, 0, 0, 0, s), "postprocess");
-        STEP(aria_k_add(h->dout, h->dout, h->dtmp, nxc, s), "k_add (postprocess)");
-    }
+    for (int b = 0; b < nb; b++)
+        if ((rc = io_gemm(h, h->dout + (size_t)b * T * C, h->dseq + ((size_t)b * S + Mt) * E, h->pout, rows, E, C, 0, s)))
+            return rc;
+    if (h->post && (rc = io_gemm(h, h->dout, h->dout, h->post, B * T, C, C, 1, s))) return rc;
     STEP(aria_k_transpose(h->dv, h->dout, T, C, B, s), "k_transpose (v)");
     return 0;
 }
