@@ -256,6 +256,9 @@ def main():
                                    "(one process per GPU, each the N = 1 path on its own rows). Run with --gpus 1."}))
         sys.exit(2)
 
+    if args.vendor:   # before this library touches the device: torch initialises HIP itself
+        print(json.dumps({"vendor": vendor_leg()}), flush=True)
+        return
     import aria_amd
     from aria_amd.device import DeviceArray, Timer
     L = aria_amd.lib()
@@ -266,9 +269,6 @@ def main():
     print(f"[bench] device: {aria_amd.device_info()}", file=sys.stderr, flush=True)
 
     rng = np.random.default_rng(SEED)
-    if args.vendor:
-        print(json.dumps({"vendor": vendor_leg()}), flush=True)
-        return
     if args.pmc_gemm:
         def run_only(fn, reps):
             for i in range(reps):
