@@ -263,6 +263,35 @@ def test_dit_sample_bitexact(hip, port):
     dit.free()
 
 
+def test_dit_sample_staging_failure(hip, port):
+    """aria_cuda_dit_sample returns -1 without running when its staging cannot be reserved (the
+    reference's caller then runs its host loop, src/aria_model_sa3.c:579-587): a schedule whose
+    per-step gcond table would need terabytes fails the device reservation; no noise is drawn, x
+    is untouched, and the handle samples normally afterwards."""
+    import ctypes as C
+    from aria_amd.dit import NOISE_FN
+    M = model(72)
+    T, n_cond, H, rot = 20, 8, 2, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = port.rope_freqs(S, rot, 10000.0)
+    x0, ced, _ = inputs(12, 1, io_ch, T, n_cond, ed)
+    dit = make_dit(M, 4, H, rot)
+    dit.set_request(T, [ced[0]], c, s)
+    calls = []
+    nz = NOISE_FN(lambda buf, n, user: calls.append(n))
+    x = x0[0].copy()
+    sched = np.linspace(1.0, 0.0, 3).astype(np.float32)
+    g = randn(rng(13), (2, 6 * ed), 0.1)
+    rc = hip.lib().aria_cuda_dit_sample(dit.h, x.ctypes.data, sched.ctypes.data, 1 << 30, g.ctypes.data,
+                                        C.cast(nz, C.c_void_p), None, None, None)
+    assert rc == -1 and not calls and np.array_equal(x, x0[0])
+    draw = rng(14)
+    got = dit.sample(x0[0], sched, g, lambda n: draw.standard_normal(n).astype(np.float32))
+    assert np.isfinite(got).all() and not np.array_equal(got, x0[0])
+    dit.free()
+
+
 def test_dit_create_rejects(hip):
     """unsupported shapes return NULL with an error (the caller falls back to the CPU DiT)."""
     from aria_amd import HipError
