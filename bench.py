@@ -553,11 +553,47 @@ def block_leg(DeviceArray, time_loop, stream, rng, reps):
         ffrows = 2 * inner if ffn == FFN_GLU else inner
         flop = 2.0 * M * dim * (3 * dim + dim + dim + dim) + 2.0 * M * dim * (ffrows + inner) \
             + 2 * 2.0 * Bb * H * Sb * Sb * 64 + 2 * 2.0 * Bb * H * Sb * Sc * 64
+        roof = block_roofline_us(ffn == FFN_GLU, prec == Q8A8, Bb, Sb, Sc, dim, H, inner)
         out[name] = {"us": round(ms * 1e3, 1), "us_min": round(ms_min * 1e3, 1),
                      "TFLOP/s": round(flop / (ms * 1e-3) / 1e12, 1), "flop": flop,
-                     "weight_bytes": blk.weight_bytes}
+                     "weight_bytes": blk.weight_bytes, "roofline_sum_us": round(roof, 1),
+                     "frac_of_roofline_sum": round(roof / (ms * 1e3), 3)}
         blk.free()
     return out
+
+
+def block_roofline_us(glu, w8, B, S, Sc, dim, H, inner):
+    """The sum of the block's per-kernel roofline times (the C4 yardstick): for every launch of
+    the forward, max(flop / MFMA peak, HBM bytes / 8 TB/s), with the bytes that launch must move:
+    fp32 residual reads and read-modify-writes, GEMM activations in fp16 (q4 block) or int8 plus
+    a row scale (W8A8), packed weights (Q8 / Q4 per the recipe; Q8 everywhere in W8A8), outputs
+    as the kernels write them (fp16 heads and attention output; fp32 attention output and FFN
+    product for the W8A8 quantiser passes, which are launches of their own there). Attention
+    runs on the fp16 MFMA peak, W8A8 GEMMs on the int8 one."""
+    M, F16, F32 = B * S, 2, 4
+    act = 1 if w8 else 2
+    peak_g = (INT8_PEAK_TOPS if w8 else FP16_PEAK_TFLOPS) * 1e12
+    peak_a, bw = FP16_PEAK_TFLOPS * 1e12, HBM_PEAK_GBS * 1e9
+    q8w = lambda N, K: N * K + 4 * N
+    q4w = lambda N, K: N * (K // 2) + 4 * N * 2 * (K // 32)
+    ffw = q8w if w8 else q4w
+    ffrows = 2 * inner if glu else inner
+    norm = (0.0, M * dim * F32 + M * dim * act + (4 * M if w8 else 0), peak_g)
+    quant = lambda K: (0.0, M * K * F32 + M * K + 4 * M, peak_g)
+    att_out = F32 if w8 else F16
+    ks = [norm,
+          (2.0 * M * dim * 3 * dim, M * dim * act + q8w(3 * dim, dim) + 3 * M * dim * F16, peak_g),
+          (4.0 * B * H * S * S * 64, 3 * M * dim * F16 + M * dim * att_out, peak_a)]
+    ks += [quant(dim)] if w8 else []
+    ks += [(2.0 * M * dim * dim, M * dim * act + q8w(dim, dim) + 2 * M * dim * F32, peak_g), norm,
+           (2.0 * M * dim * dim, M * dim * act + q8w(dim, dim) + M * dim * F16, peak_g),
+           (4.0 * B * H * S * Sc * 64, M * dim * F16 + 2 * B * H * Sc * 64 * F16 + M * dim * att_out, peak_a)]
+    ks += [quant(dim)] if w8 else []
+    ks += [(2.0 * M * dim * dim, M * dim * act + q8w(dim, dim) + 2 * M * dim * F32, peak_g), norm,
+           (2.0 * M * dim * ffrows, M * dim * act + ffw(ffrows, dim) + M * inner * (F32 if w8 else F16), peak_g)]
+    ks += [quant(inner)] if w8 else []
+    ks += [(2.0 * M * inner * dim, M * inner * act + ffw(dim, inner) + 2 * M * dim * F32, peak_g)]
+    return sum(max(f / pk, b / bw) for f, b, pk in ks) * 1e6
 
 
 def vendor_leg(reps=50):
