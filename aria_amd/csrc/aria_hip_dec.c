@@ -17,13 +17,13 @@
  *   on the chunks of the haloed sequence (the midpoint shift, src/aria_taae.c:169-205);
  *   seq sits 17 rows into a buffer of L + 34 rows, so the shifted pass runs in place and
  *   nothing is copied back. Per block (src/aria_taae.c:93-162):
- *     h16    = dyt(seq, pre_norm)                      k_dec_dyt
+ *     h16    = dyt(seq, pre_norm)                      k_dec_dyt (block 0; later blocks get it
+ *                                                      from the previous ff_out's epilogue)
  *     qkv    = h16 . to_qkv^T                          k_qgemm
  *     m16    = diff-attention per (chunk, head)        k_dec_attn
- *     seq   += m16 . to_out^T                          k_qgemm (ADD epilogue)
- *     h16    = dyt(seq, ff_norm)                       k_dec_dyt
+ *     seq   += m16 . to_out^T; h16 = dyt(seq, ff_norm) k_qgemm (ADD_DYT epilogue)
  *     g16    = silu(gate) * value of h16 . ff_in^T + b k_qgemm (GLU epilogue)
- *     seq   += g16 . ff_out^T + b                      k_qgemm (ADD epilogue)
+ *     seq   += g16 . ff_out^T + b; h16 = dyt(seq, next pre_norm)  k_qgemm (ADD_DYT / ADD)
  *   xc   = im2col of the last 16 of each group          k_dec_im2col (first T * 16 rows)
  *   audio = unpatch(xc . mapping^T + b)                 k_dec_map (fp32 MFMA)
  * The workspace is kept on the handle and grown when a longer latent arrives.
@@ -250,37 +250,65 @@ static int gemm(void *y, int y_f16, const uint16_t *x, const uint16_t *w, const 
     return 0;
 }
 
-/* one block on the nch chunks of 34 rows at x, in place (src/aria_taae.c:93-162) */
-static int block(const aria_cuda_dec *h, const dec_blk *b, const dec_ws *w, float *x, int nch, hipStream_t s) {
+/* x += m16 . W^T (+ b), and h16 = half(dyt(x, alpha, g, be)) of the new x, in the GEMM's
+ * epilogue (the next DynamicTanh norm's operand; tanh as tanh_fast) */
+static int gemm_add_dyt(float *x, const uint16_t *m16, const uint16_t *w, const float *b, int M, int K, uint16_t *h16,
+                        float alpha, const float *g, const float *be, hipStream_t s) {
+    aria_qgemm_epi e;
+    memset(&e, 0, sizeof e);
+    e.mode = ARIA_EPI_ADD_DYT;
+    e.rows_per_batch = M;
+    e.dst[0] = h16;
+    e.w[0] = g;
+    e.w[1] = be;
+    e.eps = alpha;
+    STEP(aria_k_qgemm_e(x, 0, m16, 1, ARIA_WF16, w, NULL, b, M, K, DD, 0, 0, &e, s), "k_qgemm (decoder + DyT)");
+    return 0;
+}
+
+/* one block on the nch chunks of 34 rows at x, in place (src/aria_taae.c:93-162). h16 (rows
+ * aligned with x) holds dyt(x, pre_norm) on entry; the to_out GEMM's epilogue writes
+ * dyt(x, ff_norm) into it, and ff_out's writes the next block's pre_norm DyT when `next` is given
+ * (plain residual add otherwise) */
+static int block(const aria_cuda_dec *h, const dec_blk *b, const dec_blk *next, const dec_ws *w, float *x,
+                 uint16_t *h16, int nch, hipStream_t s) {
     const int N = nch * DS;
     int rc;
-    STEP(aria_k_dec_dyt(w->h16, x, b->pre_alpha, b->pre_g, b->pre_b, N, s), "k_dec_dyt (pre_norm)");
-    if ((rc = gemm(w->qkv, 0, w->h16, b->to_qkv, NULL, N, DD, DQKV, ARIA_EPI_STORE, s))) return rc;
+    if ((rc = gemm(w->qkv, 0, h16, b->to_qkv, NULL, N, DD, DQKV, ARIA_EPI_STORE, s))) return rc;
     STEP(aria_k_dec_attn(w->m16, w->qkv, b->qn_alpha, b->qn_g, b->qn_b, b->kn_alpha, b->kn_g, b->kn_b, h->rcos,
                          h->rsin, nch, s), "k_dec_attn");
-    if ((rc = gemm(x, 0, w->m16, b->to_out, NULL, N, DD, DD, ARIA_EPI_ADD, s))) return rc;
-    STEP(aria_k_dec_dyt(w->h16, x, b->ff_alpha, b->ff_g, b->ff_b, N, s), "k_dec_dyt (ff_norm)");
-    if ((rc = gemm(w->g16, 1, w->h16, b->ff_in, b->ff_in_b, N, DD, 2 * DINNER, ARIA_EPI_GLU, s))) return rc;
+    if ((rc = gemm_add_dyt(x, w->m16, b->to_out, NULL, N, DD, h16, b->ff_alpha, b->ff_g, b->ff_b, s))) return rc;
+    if ((rc = gemm(w->g16, 1, h16, b->ff_in, b->ff_in_b, N, DD, 2 * DINNER, ARIA_EPI_GLU, s))) return rc;
+    if (next) return gemm_add_dyt(x, w->g16, b->ff_out, b->ff_out_b, N, DINNER, h16, next->pre_alpha, next->pre_g,
+                                  next->pre_b, s);
     return gemm(x, 0, w->g16, b->ff_out, b->ff_out_b, N, DINNER, DD, ARIA_EPI_ADD, s);
 }
 
-/* the device part of the decode: latent [256, T] -> audio [2, T * 4096], device pointers */
+/* the device part of the decode: latent [256, T] -> audio [2, T * 4096], device pointers. The
+ * norm operands h16 are indexed like the haloed buffer (row 17 = the sequence's row 0), so the
+ * DyT that block 2 writes for block 3 is already where the shifted pass reads it; only its halo
+ * rows are copied, as the sequence's are. */
 static int dec_run(aria_cuda_dec *h, const dec_ws *w, float *audio, const float *lat, int T, hipStream_t s) {
     const int Tp = T + (T & 1), L = 17 * Tp, Lt = 16 * T, Lout = 16 * Tp;
-    float *seq = w->seq + (size_t)DHALF * DD;   /* the sequence proper */
+    float *seq = w->seq + (size_t)DHALF * DD;      /* the sequence proper */
+    uint16_t *hseq = w->h16 + (size_t)DHALF * DD;  /* its norm operands */
     int rc;
     STEP(aria_k_dec_in(w->xt16, lat, T, h->running_std, s), "k_dec_in");
     STEP(aria_k_qgemm_e(w->x, 0, w->xt16, 1, ARIA_WF16, h->proj_w, NULL, h->proj_b, T, 256, DD, 0, 0, NULL, s),
          "k_qgemm (decoder proj)");
     STEP(aria_k_dec_expand(seq, w->x, h->new_tokens, T, Tp, s), "k_dec_expand");
+    STEP(aria_k_dec_dyt(hseq, seq, h->blk[0].pre_alpha, h->blk[0].pre_g, h->blk[0].pre_b, L, s), "k_dec_dyt (pre_norm)");
     for (int i = 0; i < 3; i++)
-        if ((rc = block(h, &h->blk[i], w, seq, L / DS, s))) return rc;
-    /* halos: [x[:17], x, x[-17:]] (src/aria_taae.c:176-183) */
+        if ((rc = block(h, &h->blk[i], &h->blk[i + 1], w, seq, hseq, L / DS, s))) return rc;
+    /* halos: [x[:17], x, x[-17:]] (src/aria_taae.c:176-183), for the sequence and its operands */
     STEP(hipMemcpyAsync(w->seq, seq, (size_t)DHALF * DD * 4, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync (halo)");
     STEP(hipMemcpyAsync(seq + (size_t)L * DD, seq + (size_t)(L - DHALF) * DD, (size_t)DHALF * DD * 4,
                         hipMemcpyDeviceToDevice, s), "hipMemcpyAsync (halo)");
+    STEP(hipMemcpyAsync(w->h16, hseq, (size_t)DHALF * DD * 2, hipMemcpyDeviceToDevice, s), "hipMemcpyAsync (halo)");
+    STEP(hipMemcpyAsync(hseq + (size_t)L * DD, hseq + (size_t)(L - DHALF) * DD, (size_t)DHALF * DD * 2,
+                        hipMemcpyDeviceToDevice, s), "hipMemcpyAsync (halo)");
     for (int i = 3; i < 6; i++)
-        if ((rc = block(h, &h->blk[i], w, w->seq, L / DS + 1, s))) return rc;
+        if ((rc = block(h, &h->blk[i], i < 5 ? &h->blk[i + 1] : NULL, w, w->seq, w->h16, L / DS + 1, s))) return rc;
     STEP(aria_k_dec_im2col(w->xc, seq, Lt, Lout, s), "k_dec_im2col");
     STEP(aria_k_dec_map(audio, w->xc, h->mapping_w, h->mapping_b, Lt, s), "k_dec_map (mapping + unpatch)");
     return 0;

@@ -110,8 +110,11 @@ enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2, ARIA_WI8 = 3 };
  *             kinds 0/1, copied for kind 2, and written fp16 to dst[sec] as
  *             [batch, heads, rows_per_batch, 64] (y unused)
  *   GLU       columns interleave (value, gate) pairs: y[m][c/2] = silu(gate) * value,
- *             [M, N/2], fp16 or fp32 (y_f16) (the weight rows were interleaved when packed) */
-enum { ARIA_EPI_STORE = 0, ARIA_EPI_GATE_RES = 1, ARIA_EPI_ADD = 2, ARIA_EPI_HEADS = 3, ARIA_EPI_GLU = 4 };
+ *             [M, N/2], fp16 or fp32 (y_f16) (the weight rows were interleaved when packed)
+ *   ADD_DYT   ADD, then also dst[0][m][c] = half(tanh(eps * y) * w[0][c] + w[1][c]) of the new y
+ *             (the next DynamicTanh norm's GEMM operand; eps carries alpha; fp16 weights only) */
+enum { ARIA_EPI_STORE = 0, ARIA_EPI_GATE_RES = 1, ARIA_EPI_ADD = 2, ARIA_EPI_HEADS = 3, ARIA_EPI_GLU = 4,
+       ARIA_EPI_ADD_DYT = 5 };
 typedef struct {
     int mode, rows_per_batch;
     const float *gate, *add2, *gate2;

@@ -304,6 +304,8 @@ extern "C" hipError_t aria_k_gemm_i8_t(void *y, int y_f16, const int8_t *xq, con
         a.y = (void *)a.epi.dst[0];
     } else if (a.epi.mode == ARIA_EPI_GLU) {
         if (N % 4 || a.gelu) return hipErrorInvalidValue;
+    } else if (a.epi.mode != ARIA_EPI_GATE_RES && a.epi.mode != ARIA_EPI_ADD && a.epi.mode != ARIA_EPI_STORE) {
+        return hipErrorInvalidValue;   /* ADD_DYT is the fp16-weight decoder's */
     } else if (a.epi.mode != ARIA_EPI_STORE) {
         if (y_f16 || a.epi.rows_per_batch <= 0) return hipErrorInvalidValue;
     }

@@ -466,6 +466,13 @@ extern "C" hipError_t aria_k_qgemm_e(void *y, int y_f16, const void *x, int x_f1
         a.y = (void *)a.epi.dst[0];   /* alignment check only; y is not written */
     } else if (a.epi.mode == ARIA_EPI_GLU) {
         if (N % 4 || a.gelu) return hipErrorInvalidValue;
+    } else if (a.epi.mode == ARIA_EPI_ADD_DYT) {   /* the decoder's fp16-weight GEMMs only */
+        if (wtype != ARIA_WF16 || !x_f16 || y_f16 || a.gelu || a.epi.rows_per_batch <= 0 || !a.epi.dst[0] ||
+            !a.epi.w[0] || !a.epi.w[1] || ((uintptr_t)a.epi.dst[0] & 7u) || ((uintptr_t)a.epi.w[0] & 15u) ||
+            ((uintptr_t)a.epi.w[1] & 15u))
+            return hipErrorInvalidValue;
+    } else if (a.epi.mode > ARIA_EPI_ADD_DYT || a.epi.mode < 0) {
+        return hipErrorInvalidValue;
     } else if (a.epi.mode != ARIA_EPI_STORE) {
         if (y_f16 || a.epi.rows_per_batch <= 0) return hipErrorInvalidValue;
     }

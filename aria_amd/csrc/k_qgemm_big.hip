@@ -403,6 +403,9 @@ static void launch_big(const QArgs &a, hipStream_t s) {
     switch (a.epi.mode) {
         case ARIA_EPI_GATE_RES: launch_big_m<WT, FM, FN, ARIA_EPI_GATE_RES, false, MINB>(a, s); break;
         case ARIA_EPI_ADD: launch_big_m<WT, FM, FN, ARIA_EPI_ADD, false, MINB>(a, s); break;
+        case ARIA_EPI_ADD_DYT:
+            if constexpr (WT == ARIA_WF16) launch_big_m<WT, FM, FN, ARIA_EPI_ADD_DYT, false, MINB>(a, s);
+            break;
         case ARIA_EPI_HEADS:
             if constexpr (FN >= 2) launch_big_m<WT, FM, FN, ARIA_EPI_HEADS, false, MINB>(a, s);
             break;

@@ -99,6 +99,7 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
                 if (g) epilogue<FM, FN, WT, ARIA_EPI_ADD, true>(a, acc, E, lane, mw, nw);
                 else epilogue<FM, FN, WT, ARIA_EPI_ADD>(a, acc, E, lane, mw, nw);
                 return;
+            case ARIA_EPI_ADD_DYT: epilogue<FM, FN, WT, ARIA_EPI_ADD_DYT>(a, acc, E, lane, mw, nw); return;   /* no GELU */
             case ARIA_EPI_HEADS:
                 if constexpr (LPR % 16 == 0) {
                     if (g) epilogue<FM, FN, WT, ARIA_EPI_HEADS, true>(a, acc, E, lane, mw, nw);
@@ -238,9 +239,16 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
                 else   /* fp32 (the W8A8 block quantises the fp32 product) */
                     *reinterpret_cast<float2 *>((float *)a.y + (size_t)m * (a.N >> 1) + (nb >> 1)) = make_float2(g0, g1);
             }
-        } else if constexpr (MODE == ARIA_EPI_GATE_RES || MODE == ARIA_EPI_ADD) {
+        } else if constexpr (MODE == ARIA_EPI_GATE_RES || MODE == ARIA_EPI_ADD || MODE == ARIA_EPI_ADD_DYT) {
             /* read-modify-write of the fp32 residual: all loads first, then all stores */
             float4 rr[NIT], g2[NIT];
+            float4 dg = make_float4(0.f, 0.f, 0.f, 0.f), db = dg;   /* ADD_DYT: the norm's gain and bias */
+            if constexpr (MODE == ARIA_EPI_ADD_DYT) {
+                if (col_ok) {
+                    dg = *reinterpret_cast<const float4 *>(e.w[0] + nb);
+                    db = *reinterpret_cast<const float4 *>(e.w[1] + nb);
+                }
+            }
             const int nbc = col_ok ? nb : 0;
 #pragma unroll
             for (int it = 0; it < NIT; it++) {
@@ -264,9 +272,16 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
                                     rr[it].z + v[it][2] * sg.z, rr[it].w + v[it][3] * sg.w);
                 } else {
                     o = make_float4(rr[it].x + v[it][0], rr[it].y + v[it][1], rr[it].z + v[it][2], rr[it].w + v[it][3]);
-                    if (e.add2) o = make_float4(o.x + g2[it].x, o.y + g2[it].y, o.z + g2[it].z, o.w + g2[it].w);
+                    if (MODE == ARIA_EPI_ADD && e.add2)
+                        o = make_float4(o.x + g2[it].x, o.y + g2[it].y, o.z + g2[it].z, o.w + g2[it].w);
                 }
                 *reinterpret_cast<float4 *>((float *)a.y + (size_t)m * a.N + nb) = o;
+                if constexpr (MODE == ARIA_EPI_ADD_DYT) {
+                    const float al = e.eps;
+                    const float h0 = tanh_fast(al * o.x) * dg.x + db.x, h1 = tanh_fast(al * o.y) * dg.y + db.y;
+                    const float h2 = tanh_fast(al * o.z) * dg.z + db.z, h3 = tanh_fast(al * o.w) * dg.w + db.w;
+                    *reinterpret_cast<uint2 *>(e.dst[0] + (size_t)m * a.N + nb) = make_uint2(pack2h(h0, h1), pack2h(h2, h3));
+                }
             }
         } else {   /* HEADS */
             const int S = e.rows_per_batch;
