@@ -319,11 +319,11 @@ extern "C" hipError_t aria_k_gemm_i8_t(void *y, int y_f16, const int8_t *xq, con
         return hipGetLastError();
     }
     if (fm >= 16) return qgemm_big_i8_launch(a, fm - 16, s);   /* the LDS-DMA kernel, configuration fm - 16 */
-    if (fm <= 0 && K % 128 == 0 && N <= 3072) {
-        /* the LDS-DMA kernel (k_qgemm_big.hip) where it measured faster: N <= 1024 (64-row tiles,
-         * two workgroups per CU; HEADS in 64 x 256) and the N <= 3072 projections (128 x 256) */
-        const bool heads = a.epi.mode == ARIA_EPI_HEADS;
-        return qgemm_big_i8_launch(a, N <= 1024 ? (heads ? 1 : 0) : 2, s);
+    const bool heads = a.epi.mode == ARIA_EPI_HEADS;
+    if (fm <= 0 && K % 128 == 0 && (!heads || N <= 3072)) {
+        /* the LDS-DMA kernel (k_qgemm_big.hip), two workgroups per CU, at every DiT shape:
+         * HEADS in 64 x 256, N <= 1024 in 64 x 128, N <= 3072 in 128 x 128, wider in 192 x 128 */
+        return qgemm_big_i8_launch(a, heads ? 1 : N <= 1024 ? 0 : N <= 3072 ? 2 : 3, s);
     }
     if (fm <= 0) {
         /* tile rows, from a sweep at M = 2592 (fm: 1..4 = 32..128 rows): 128 rows when those

@@ -387,12 +387,14 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
     epilogue<FM, FN, WT, MODE, GELU, AccT>(a, acc, E, lane, m0, n0 + wave * 32 * FN);
 }
 
-template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int NS = 1, int NST = 3>
+/* NST = 0: three stages where they fit the LDS share of MINB workgroups, else two */
+template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int NS = 1, int NST = 0>
 static void launch_big_m(const QArgs &a, hipStream_t s) {
     constexpr int BM = 32 * FM, BN = 128 * FN;
+    constexpr int NSTA = NST ? NST : (3 * NS * Stage<WT, FM, FN>::BYTES <= (MINB == 1 ? 160 : 80) * 1024 ? 3 : 2);
     const int MT = (a.M + BM - 1) / BM, NTN = (a.N + BN - 1) / BN, T = MT * NTN;
     const int grid = ((T + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_qgemm_big<WT, FM, FN, MODE, GELU, MINB, NS, NST>), dim3(grid), dim3(256), 0, s, a, NTN, T);
+    hipLaunchKernelGGL((k_qgemm_big<WT, FM, FN, MODE, GELU, MINB, NS, NSTA>), dim3(grid), dim3(256), 0, s, a, NTN, T);
 }
 
 /* one kernel per fused epilogue mode (a run-time mode switch inside the store loop makes
@@ -420,14 +422,19 @@ static void launch_big(const QArgs &a, hipStream_t s) {
 /* the configurations compiled (FM, FN, workgroups per CU), index = the cfg argument; measured
  * at M = 2592 (DiT shapes), fp16 activations:
  *   0: 96 x 128, two per CU: N <= 1024 (sa_out, ca_out, ff_out; K = 1024 and 4096)
- *   1: 128 x 256, one per CU (explicit requests)
- *   2: 128 x 128, two per CU: N = 3072 without HEADS
- *   3: 64 x 256, two per CU: the HEADS projections (qkv N = 3072, ca_q N = 1024): a head's 64
+ *   1: 128 x 128, two per CU: N = 3072 without HEADS
+ *   2: 64 x 256, two per CU: the HEADS projections (qkv N = 3072, ca_q N = 1024): a head's 64
  *      columns in one wave, and the second workgroup per CU covers the other's HEADS epilogue
- *      (block 214 -> 204 us against 128 x 256 for qkv and the weights-in-registers ca_q) */
-#define BIG_CFGS(X) X(0, 3, 1, 2) X(1, 4, 2, 1) X(2, 4, 1, 2) X(3, 2, 2, 2)
-static const int big_fm[] = {3, 4, 4, 2};
-static const int big_fn[] = {1, 2, 1, 2};
+ *      (block 214 -> 204 us against 128 x 256 for qkv and the weights-in-registers ca_q)
+ *   3: 192 x 128, two per CU in two stages: N = 4096 (ff_in; 448 tiles fill the 512 slots
+ *      once; Q8 36.5 -> 33.3 us, Q4 38.2 -> 36.0 us against the weights-in-registers kernel)
+ *   4: 224 x 128, two per CU in two stages: N > 4096 (the GLU ff_in, N = 8192: Q8 74.4 ->
+ *      58.3 us, Q4 73.4 -> 63.5 us)
+ * Larger FM amortises each unpacked weight over more rows; 96 x 256, 64 x 128 and 192 x 256
+ * (one per CU) measured slower at every DiT shape. */
+#define BIG_CFGS(X) X(0, 3, 1, 2) X(1, 4, 1, 2) X(2, 2, 2, 2) X(3, 6, 1, 2) X(4, 7, 1, 2)
+static const int big_fm[] = {3, 4, 2, 6, 7};
+static const int big_fn[] = {1, 1, 2, 1, 1};
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
 
@@ -475,10 +482,14 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
 /* W8A8 (int8 activations, Q8 weights, K % 128 == 0): the configurations compiled, index = cfg,
  * measured at M = 2592 against the weights-in-registers int8 kernel (k_gemm_i8.hip):
  *   0: 64 x 128, two workgroups per CU: N <= 1024 (K = 1024: 14.6 -> 9.9 us; K = 4096: 39.4 -> 23.4 us)
- *   1: 64 x 256: N <= 1024 with HEADS (a head's 64 columns in one wave)
- *   2: 128 x 256: 1024 < N <= 3072 (the qkv projection: 22.2 -> 19.3 us) */
-#define BIG_I8_CFGS(X) X(0, 2, 1, 2) X(1, 2, 2, 1) X(2, 4, 2, 1)
-int qgemm_big_i8_ncfg() { return 3; }
+ *   1: 64 x 256, two per CU in two stages: HEADS (qkv and ca_q; W8A8 block 192.7 -> 188.0 us
+ *      against 128 x 256 one per CU for qkv and 64 x 256 one per CU for ca_q)
+ *   2: 128 x 128, two per CU in two stages: 1024 < N <= 3072 (N = 3072: 19.5 -> 17.6 us
+ *      against 128 x 256 one per CU)
+ *   3: 192 x 128, two per CU in two stages: N > 3072 (ff_in N = 4096: 29.3 -> 22.7 us;
+ *      the GLU ff_in N = 8192: 61.4 -> 49.6 us) */
+#define BIG_I8_CFGS(X) X(0, 2, 1, 2) X(1, 2, 2, 2) X(2, 4, 1, 2) X(3, 6, 1, 2)
+int qgemm_big_i8_ncfg() { return 4; }
 
 hipError_t qgemm_big_i8_launch(const QArgs &a, int cfg, hipStream_t s) {
     if (a.K % 128 || (a.gelu && a.epi.mode != ARIA_EPI_STORE)) return hipErrorInvalidValue;
