@@ -400,14 +400,13 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
         return hipGetLastError();
     } else {
     if constexpr (WT == ARIA_WF16) {
-        /* fp16 weights on the LDS-DMA kernel: explicit tiles 13.., or picked for N <= 1024
-         * (64 x 128 tiles, two per CU), where it measured 10-17 % faster than the LDS-operand
-         * kernel on the decoder's to_out / ff_out (M 1870 and 11016, K 768 and 2304); wider N
-         * stays on the LDS-operand kernel's 128 x 128 / 192 x 128 tiles */
+        /* fp16 weights on the LDS-DMA kernel: explicit tiles 13.., or the configuration that
+         * qgemm_big_f16_pick chooses for the shape (HEADS, which needs 64 columns per wave,
+         * stays on the LDS-operand kernel) */
         if (tiles >= 13) return qgemm_big_launch(a, WT, tiles - 13, s);
-        if (tiles == 0 && a.N <= 1024 && a.K % 64 == 0 && (!a.gelu || a.epi.mode == ARIA_EPI_STORE) &&
+        if (tiles == 0 && a.K % 64 == 0 && (!a.gelu || a.epi.mode == ARIA_EPI_STORE) &&
             a.epi.mode != ARIA_EPI_HEADS)
-            return qgemm_big_launch(a, WT, 0, s);
+            return qgemm_big_launch(a, WT, qgemm_big_f16_pick(a.M, a.N), s);
     }
     if constexpr (WT != ARIA_WF16) {
         /* the LDS-DMA kernel (k_qgemm_big.hip): explicit tiles 13.. (configuration tiles - 13),

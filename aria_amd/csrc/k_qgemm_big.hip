@@ -438,11 +438,29 @@ static const int big_fn[] = {1, 1, 2, 1, 1};
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
 
-/* fp16 weights (the decoder's GEMMs): 128-byte weight rows per K-tile, twice the Q8 bytes, so
- * the tiles are those that fit three stages: index = cfg
- *   0: 64 x 128, two workgroups per CU    1: 64 x 256    2: 128 x 256    3: 128 x 128 */
-#define BIG_F16_CFGS(X) X(0, 2, 1, 2) X(1, 2, 2, 1) X(2, 4, 2, 1) X(3, 4, 1, 1)
-static const int big_f16_fn[] = {1, 2, 2, 1};
+/* fp16 weights (the decoder's GEMMs): 128-byte weight rows per K-tile, twice the Q8 bytes.
+ * index = cfg: BM = 64, 96, 128, 160, 192 rows by 128 weight rows, two workgroups per CU (the
+ * first in three stages, the others in two). qgemm_big_f16_pick chooses by a cost model fitted
+ * to the decoder's GEMMs (M = 1870 and 11016; N / K = 3840 / 768, 4608 / 768, 768 / 768,
+ * 768 / 2304): the CU with the most tiles, ceil(T / 256) of them, times the tile's rows times
+ * a per-row time that falls with BM (each LDS weight fragment feeds more MFMAs). It picks the
+ * fastest configuration at all eight shapes; against the LDS-operand kernel's 192 x 128
+ * tiles: 105.6 -> 97.0 us (N = 3840), 136.7 -> 119.8 us (N = 4608) at M = 11016. */
+#define BIG_F16_CFGS(X) X(0, 2, 1, 2) X(1, 3, 1, 2) X(2, 4, 1, 2) X(3, 5, 1, 2) X(4, 6, 1, 2)
+static const int big_f16_fn[] = {1, 1, 1, 1, 1};
+
+int qgemm_big_f16_pick(int M, int N) {
+    static const float row_us[5] = {0.088f, 0.092f, 0.082f, 0.075f, 0.070f};   /* FM = 2 .. 6 */
+    int best = 0;
+    float best_c = 1e30f;
+    for (int c = 0; c < 5; c++) {
+        const int bm = 32 * (c + 2);
+        const long T = (long)((M + bm - 1) / bm) * ((N + 127) / 128);
+        const float cost = (float)((T + 255) / 256) * (float)bm * row_us[c];
+        if (cost < best_c) { best_c = cost; best = c; }
+    }
+    return best;
+}
 
 static hipError_t qgemm_big_f16_launch(const QArgs &a, int cfg, hipStream_t s) {
     if (cfg < 0 || cfg >= (int)(sizeof big_f16_fn / sizeof big_f16_fn[0]) ||

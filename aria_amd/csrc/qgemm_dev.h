@@ -346,6 +346,8 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s);
 int qgemm_big_ncfg();
 int qgemm_big_bm(int cfg);
 int qgemm_big_bn(int cfg);
+/* the fp16-weight configuration for an M x N product (any K) */
+int qgemm_big_f16_pick(int M, int N);
 /* its W8A8 form (int8 activations with per-row scales in a.xscale, Q8 weights, K % 128 == 0) */
 hipError_t qgemm_big_i8_launch(const QArgs &a, int cfg, hipStream_t s);
 int qgemm_big_i8_ncfg();
