@@ -77,6 +77,36 @@ __global__ __launch_bounds__(256) void k_quant_act_q8(int8_t *xq, float *sx, con
     if (lane == 0) sx[row] = mx / 127.0f;
 }
 
+/* rows of 2048 <= K <= 8192, K % 1024 == 0 (the FFN product): one 256-lane workgroup per
+ * row, lane t holding elements 4 (t + 256 j), j < K / 1024, so four waves share a row's
+ * latency instead of one wave walking 16 vectors per lane; the four wave maxima meet in LDS
+ * (a maximum is exact in any order, so the bits equal the one-wave kernel's) */
+template <bool F16>
+__global__ __launch_bounds__(256) void k_quant_act_q8_row(int8_t *xq, float *sx, const void *x, int K) {
+    __shared__ float wmax[4];
+    const int row = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const size_t base = (size_t)row * K;
+    const int nv = K >> 10;
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (j < nv) v[j] = qa_load<F16>(x, base + 4 * (t + 256 * j));
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (j < nv) mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
+    mx = grp_max<64>(mx);
+    if (lane == 0) wmax[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+    uint32_t *qr = reinterpret_cast<uint32_t *>(xq + base);
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (j < nv) qr[t + 256 * j] = q8_pack4(v[j], inv);
+    if (t == 0) sx[row] = mx / 127.0f;
+}
+
 /* ---- int8 GEMM, weights in registers ----
  * 4 waves share one int8 activation tile of BM = 32 FM rows x 64 k in LDS (double
  * buffered); wave w owns weight rows n0 + 64 w .. + 63 (two 32-row MFMA blocks) and loads
@@ -281,6 +311,11 @@ extern "C" hipError_t aria_k_quant_act_q8(int8_t *xq, float *sx, const void *x, 
                                           hipStream_t s) {
     if (M <= 0) return hipSuccess;
     if (K <= 0) return hipErrorInvalidValue;
+    if (K % 1024 == 0 && K >= 2048 && K <= 8192) {
+        if (x_f16) hipLaunchKernelGGL(k_quant_act_q8_row<true>, dim3(M), dim3(256), 0, s, xq, sx, x, K);
+        else hipLaunchKernelGGL(k_quant_act_q8_row<false>, dim3(M), dim3(256), 0, s, xq, sx, x, K);
+        return hipGetLastError();
+    }
     const int grid = (M + 3) / 4;
     if (x_f16) hipLaunchKernelGGL(k_quant_act_q8<true>, dim3(grid), dim3(256), 0, s, xq, sx, x, M, K);
     else hipLaunchKernelGGL(k_quant_act_q8<false>, dim3(grid), dim3(256), 0, s, xq, sx, x, M, K);

@@ -66,6 +66,31 @@ def test_w8a8_config3_full(ops, port, KN):
     assert np.array_equal(bits(y[rows]), bits(want))
 
 
+@pytest.mark.parametrize("K", [256, 1024, 1031, 2048, 3072, 4096, 5000, 8192])
+@pytest.mark.parametrize("f16", [0, 1])
+def test_quant_act_q8_rows(hip, port, K, f16):
+    """The activation quantiser on both of its row mappings (one wave per row; one workgroup
+    per row for 2048 <= K <= 8192, K % 1024 == 0) and its scalar forms, fp32 and fp16 input:
+    int8 rows and scales bit-identical to or_quant_act_q8, with a zero row and rows whose
+    maximum sits in the first or the last element."""
+    from aria_amd.device import DeviceArray, sync
+    L = hip.lib()
+    r = rng(4000 + K + f16)
+    M = 37
+    x = randn(r, (M, K))
+    x[3] = 0.0
+    x[5, 0] = 50.0
+    x[6, K - 1] = -60.0
+    xin = x.astype(np.float16) if f16 else x
+    xq_want, sx_want = port.quant_act_q8(np.ascontiguousarray(xin, np.float32))
+    dx = DeviceArray.from_host(xin)
+    dxq, dsx = DeviceArray((M, K), np.int8), DeviceArray((M,), np.float32)
+    hip.check(L.aria_hip_quant_act_q8_dev(dxq.p, dsx.p, dx.p, f16, M, K, None))
+    sync()
+    assert np.array_equal(dxq.to_host(), xq_want)
+    assert np.array_equal(bits(dsx.to_host()), bits(sx_want))
+
+
 def test_w8a8_device_api(hip, port):
     """fp16 activations (what the fused norms emit), fp16 outputs, and the composite entry
     with caller workspace, through the device-pointer ABI."""
