@@ -83,29 +83,48 @@ struct DecAttnArgs {
 /* ---- the chunk attention on the fp32 MFMA (v_mfma_f32_16x16x4_f32) ----
  * One (chunk, head) per workgroup of two waves; wave w computes pair w (0: q, k; 1: qd, kd)
  * over the chunk's 34 tokens padded to 48 (3 blocks of 16):
+ *   v (34 rows x 64 dims, shared by both pairs) travels to LDS by LDS DMA first thing, so
+ *     its fetch overlaps the q / k work and takes no registers
  *   S = q k^T: 3 x 3 blocks, 16 k-steps; lane l supplies row l % 16 of q (A) and of k (B) at
  *     dim 16 (l / 16) + s in step s, so each lane loads 16 consecutive dims of one row from
  *     qkv, applies the DynamicTanh norm and RoPE in registers (the rotation's partner dim
  *     d +- 16 sits in lane l ^ 16, same row) and keeps them as its operands
  *   softmax over the 34 valid keys in the accumulators (a row's 16 columns of a block sit in
  *     16 lanes: xor-shuffle reductions), probabilities through LDS into the A layout
- *   O = P v: 3 x 4 blocks, 12 k-steps over keys 12 (l / 16) + s, v read from qkv
- * Wave 1 leaves O in LDS (lane-major), wave 0 writes half(O0 - O1) to the merged rows.
- * Accumulator v of lane l in a 16 x 16 block: row 4 (l / 16) + v, column l % 16. Padded q / k
- * rows are zero and padded keys are masked before the max, so nothing past the chunk's rows
- * is read. fp32 operands, as the reference keeps this attention fp32. */
+ *   O = P v: 3 x 4 blocks, 12 k-steps over keys 12 (l / 16) + s; output block j column n
+ *     holds dim 4 n + j, so a lane's B operands of a step are one 16-byte LDS read of v and
+ *     its four output dims of a row are adjacent (one 8-byte store)
+ * Wave 1 leaves O in LDS (lane-major, over the v / P space once both products are done),
+ * wave 0 writes half(O0 - O1) to the merged rows. Accumulator v of lane l in a 16 x 16
+ * block: row 4 (l / 16) + v, column l % 16. Padded q / k rows are zero and padded keys are
+ * masked before the max and multiply zero v, so nothing past the chunk's rows is used. fp32
+ * operands, as the reference keeps this attention fp32. */
 #define DA_P 48            /* padded chunk */
 #define DA_PS 52           /* LDS row stride of P (floats; 16-byte aligned rows) */
+#define DA_VCH 576         /* v staging: 16-byte chunks (34 rows x 16, rounded up to 9 x 64) */
 
 typedef float f32x4_dec __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
-    __shared__ __attribute__((aligned(16))) float Ps[2][DA_P * DA_PS];
-    __shared__ float Os[48 * 64];
+    /* [0, 9216): v rows (256 B each); [9216, 9216 + 2 * 48 * 52 * 4): P of the two waves;
+     * after both products: O of wave 1 (48 x 64 floats, lane-major) from offset 0 */
+    __shared__ __attribute__((aligned(16))) float sm[DA_VCH * 4 + 2 * DA_P * DA_PS];
+    float4 *Vs = reinterpret_cast<float4 *>(sm);
     const int ch = blockIdx.x / H, h = blockIdx.x % H;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int lr = lane & 15, lq = lane >> 4;
     const float *base = a.qkv + (size_t)ch * DEC_S * DEC_QKV + h * DEC_HD;
+
+    /* v by LDS DMA: instruction i moves chunks 64 i .. 64 i + 63 (row p / 16, dims 4 (p % 16)
+     * ..), wave w the instructions i = w, w + 2, ..; chunks past the 34 rows re-read row 33 */
+    {
+        typedef __attribute__((address_space(3))) void lds_void_t;
+        for (int i = wave; i < DA_VCH / 64; i += 2) {
+            const int p = 64 * i + lane, r = min(p >> 4, DEC_S - 1);
+            __builtin_amdgcn_global_load_lds(base + (size_t)r * DEC_QKV + 1536 + 4 * (p & 15),
+                                             (lds_void_t *)(sm + 256 * i), 16, 0, 0);
+        }
+    }
 
     /* this lane's 16 dims (16 lq ..) of q (or qd) and k (or kd) rows 16 b + lr, normalised
      * and rotated */
@@ -114,9 +133,15 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
         const int qo = wave ? 2304 : 0, ko = wave ? 3072 : 768;
         float qg[16], qb[16], kg[16], kb[16];
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            qg[j] = a.qg[lq * 16 + j]; qb[j] = a.qb[lq * 16 + j];
-            kg[j] = a.kg[lq * 16 + j]; kb[j] = a.kb[lq * 16 + j];
+        for (int j4 = 0; j4 < 4; j4++) {
+            const float4 g0 = reinterpret_cast<const float4 *>(a.qg + lq * 16)[j4];
+            const float4 b0 = reinterpret_cast<const float4 *>(a.qb + lq * 16)[j4];
+            const float4 g1 = reinterpret_cast<const float4 *>(a.kg + lq * 16)[j4];
+            const float4 b1 = reinterpret_cast<const float4 *>(a.kb + lq * 16)[j4];
+            qg[4 * j4] = g0.x; qg[4 * j4 + 1] = g0.y; qg[4 * j4 + 2] = g0.z; qg[4 * j4 + 3] = g0.w;
+            qb[4 * j4] = b0.x; qb[4 * j4 + 1] = b0.y; qb[4 * j4 + 2] = b0.z; qb[4 * j4 + 3] = b0.w;
+            kg[4 * j4] = g1.x; kg[4 * j4 + 1] = g1.y; kg[4 * j4 + 2] = g1.z; kg[4 * j4 + 3] = g1.w;
+            kb[4 * j4] = b1.x; kb[4 * j4 + 1] = b1.y; kb[4 * j4 + 2] = b1.z; kb[4 * j4 + 3] = b1.w;
         }
 #pragma unroll
         for (int b = 0; b < 3; b++) {
@@ -137,17 +162,25 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
             }
             /* RoPE on dims 0..31: lanes lq = 0 hold d < 16, lq = 1 hold d + 16 */
             const int rc = ok ? r : 0;
+            float cs[16], sn[16];
+#pragma unroll
+            for (int j4 = 0; j4 < 4; j4++) {
+                const float4 c4 = reinterpret_cast<const float4 *>(a.rcos + rc * DEC_RH)[j4];
+                const float4 s4 = reinterpret_cast<const float4 *>(a.rsin + rc * DEC_RH)[j4];
+                cs[4 * j4] = c4.x; cs[4 * j4 + 1] = c4.y; cs[4 * j4 + 2] = c4.z; cs[4 * j4 + 3] = c4.w;
+                sn[4 * j4] = s4.x; sn[4 * j4 + 1] = s4.y; sn[4 * j4 + 2] = s4.z; sn[4 * j4 + 3] = s4.w;
+            }
 #pragma unroll
             for (int j = 0; j < 16; j++) {
                 const float pq = __shfl_xor(qf[b][j], 16), pk = __shfl_xor(kf[b][j], 16);
                 if (lq < 2) {
-                    const float c = a.rcos[rc * DEC_RH + j], sn = a.rsin[rc * DEC_RH + j];
+                    const float c = cs[j], sv = sn[j];
                     if (lq == 0) {
-                        const float q0 = qf[b][j] * c, q1 = pq * sn, k0 = kf[b][j] * c, k1 = pk * sn;
+                        const float q0 = qf[b][j] * c, q1 = pq * sv, k0 = kf[b][j] * c, k1 = pk * sv;
                         qf[b][j] = ok ? q0 - q1 : 0.0f;
                         kf[b][j] = ok ? k0 - k1 : 0.0f;
                     } else {
-                        const float q0 = qf[b][j] * c, q1 = pq * sn, k0 = kf[b][j] * c, k1 = pk * sn;
+                        const float q0 = qf[b][j] * c, q1 = pq * sv, k0 = kf[b][j] * c, k1 = pk * sv;
                         qf[b][j] = ok ? q0 + q1 : 0.0f;
                         kf[b][j] = ok ? k0 + k1 : 0.0f;
                     }
@@ -171,7 +204,7 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
                 sc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[i][st], kf[j][st], sc[i][j], 0, 0, 0);
 
     /* softmax of each row over keys < 34 (block 2 holds keys 32 + lr) */
-    float *P = Ps[wave];
+    float *P = sm + DA_VCH * 4 + wave * (DA_P * DA_PS);
 #pragma unroll
     for (int i = 0; i < 3; i++)
 #pragma unroll
@@ -192,21 +225,17 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
             P[row * DA_PS + 32 + lr] = x2 * inv;
         }
 
-    /* O = P v over keys 12 lq + s (keys >= 34 have P = 0 and read no v) */
+    /* v in LDS: this wave's transfers done (vmcnt), then the barrier publishes both waves' */
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+
+    /* O = P v over keys 12 lq + s (keys >= 34 have P = 0 and multiply zero v) */
     f32x4_dec oc[3][4];
 #pragma unroll
     for (int i = 0; i < 3; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) oc[i][j] = f32x4_dec{0.0f, 0.0f, 0.0f, 0.0f};
     {
-        float vf[4][12];
-#pragma unroll
-        for (int s2 = 0; s2 < 12; s2++) {
-            const int key = lq * 12 + s2;
-            const float *vr = base + (size_t)(key < DEC_S ? key : 0) * DEC_QKV + 1536 + lr;
-#pragma unroll
-            for (int j = 0; j < 4; j++) vf[j][s2] = key < DEC_S ? vr[16 * j] : 0.0f;
-        }
         float pf[3][12];
 #pragma unroll
         for (int i = 0; i < 3; i++)
@@ -216,14 +245,22 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
                 pf[i][4 * c4 + 0] = p4.x; pf[i][4 * c4 + 1] = p4.y; pf[i][4 * c4 + 2] = p4.z; pf[i][4 * c4 + 3] = p4.w;
             }
 #pragma unroll
-        for (int s2 = 0; s2 < 12; s2++)
+        for (int s2 = 0; s2 < 12; s2++) {
+            const int key = lq * 12 + s2;
+            const float4 v4 = Vs[min(key, DEC_S - 1) * 16 + lr];
+            const bool kv = key < DEC_S;
+            const float vf[4] = {kv ? v4.x : 0.0f, kv ? v4.y : 0.0f, kv ? v4.z : 0.0f, kv ? v4.w : 0.0f};
 #pragma unroll
             for (int i = 0; i < 3; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    oc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pf[i][s2], vf[j][s2], oc[i][j], 0, 0, 0);
+                    oc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pf[i][s2], vf[j], oc[i][j], 0, 0, 0);
+        }
     }
 
+    /* both products done before wave 1's O overwrites v and P */
+    __syncthreads();
+    float *Os = sm;
     if (wave == 1) {
 #pragma unroll
         for (int i = 0; i < 3; i++)
@@ -234,16 +271,17 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
     }
     __syncthreads();
     if (wave == 0) {
-        uint16_t *dst = a.merged + (size_t)ch * DEC_S * DEC_D + h * DEC_HD + lr;
+        uint2 *dst = reinterpret_cast<uint2 *>(a.merged + (size_t)ch * DEC_S * DEC_D + h * DEC_HD + 4 * lr);
 #pragma unroll
         for (int i = 0; i < 3; i++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int row = i * 16 + 4 * lq + v;
                 if (row < DEC_S) {
+                    uint32_t hv[4];
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        dst[(size_t)row * DEC_D + 16 * j] = f2h_bits(oc[i][j][v] - Os[((i * 4 + j) * 4 + v) * 64 + lane]);
+                    for (int j = 0; j < 4; j++) hv[j] = f2h_bits(oc[i][j][v] - Os[((i * 4 + j) * 4 + v) * 64 + lane]);
+                    dst[(size_t)row * (DEC_D / 4)] = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
                 }
             }
     }
