@@ -27,8 +27,8 @@
  * l is accumulated (v_dot2_f32_f16, exact products) from the same fp16 P that multiplies
  * V. The running max is a lazy reference (moved only when a tile exceeds it by 2^8), so
  * the accumulators are rarely rescaled; O / l does not depend on the reference chosen.
- * Workgroup: 4 waves x 32 queries = 128 queries of one (batch, head), or 8 waves when
- * the keys are split in two halves inside the workgroup (long key sets); K and V tiles
+ * Workgroup: QW = 3 or 4 waves x 32 queries of one (batch, head), twice the waves when the
+ * keys are split in two halves inside the workgroup (long key sets); K and V tiles
  * of 64 keys are staged key-major in LDS (swizzled, conflict-free) by LDS DMA
  * (global_load_lds_dwordx4, no staging registers), the next tile's transfer running under
  * the current tile's math; the V^T operand is read with the gfx950 transpose load
@@ -136,7 +136,7 @@ struct AttnArgs {
     const uint16_t *q, *k, *v;   /* [B*H, N, 64] fp16 */
     void *o;                     /* [B, Nq, H*64] merged heads */
     int H, Nq, Nk;
-    int nqb, T;                  /* 128-query blocks per (batch, head); nqb * B*H */
+    int nqb, T;                  /* query blocks (32 QW queries) per (batch, head); nqb * B*H */
     float scale_log2;            /* (1/sqrt(64)) * log2(e) */
     int o_f16;
 };
@@ -178,12 +178,13 @@ __device__ __forceinline__ uint32_t pack2h_rn(float x, float y) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_v));
 }
 
-/* KS = 1: 4 waves, all keys. KS = 2: 8 waves; waves 4-7 take the second half of the key
- * tiles with their own LDS buffers, and the halves merge (max, row sum, O) through LDS at
- * the end: twice the waves per query block without any exchange between workgroups. Both
- * halves run the same number of loop trips, so every barrier is reached by all waves. */
-template <int KS>
-__global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) void k_flash_attn(AttnArgs a) {
+/* QW (3 or 4) waves of 32 queries per key half. KS = 1: all keys. KS = 2: 2 QW waves; waves QW..2 QW - 1
+ * take the second half of the key tiles with their own LDS buffers, and the halves merge
+ * (max, row sum, O) through LDS at the end: twice the waves per query block without any
+ * exchange between workgroups. Both halves run the same number of loop trips, so every
+ * barrier is reached by all waves. */
+template <int KS, int QW>
+__global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(4))) void k_flash_attn(AttnArgs a) {
     /* tile buffers, each [half][KT x 64] fp16, as four separate LDS objects: K and V tiles
      * arrive by LDS DMA (global_load_lds), whose writes count on vmcnt, and the compiler only
      * omits a vmcnt wait before a fragment read when the read provably targets another object
@@ -194,16 +195,19 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
     __shared__ __attribute__((aligned(16))) uint16_t Vb0s[KS * KT * 64];
     __shared__ __attribute__((aligned(16))) uint16_t Vb1s[KS * KT * 64];
 
-    const int half = KS == 1 ? 0 : (int)(threadIdx.x >> 8);
+    static_assert(QW == 3 || QW == 4, "three or four query waves per key half");
+    /* the wave index in a scalar register: everything derived from it stays scalar */
+    const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int half = KS == 1 ? 0 : wid / QW;
     uint16_t *const Kb0 = Kb0s + half * (KT * 64), *const Kb1 = Kb1s + half * (KT * 64);
     uint16_t *const Vb0 = Vb0s + half * (KT * 64), *const Vb1 = Vb1s + half * (KT * 64);
-    const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+    const int lane = threadIdx.x & 63, wave = wid % QW, g = lane >> 5, l32 = lane & 31;
     /* the query blocks of one (batch, head) run on one XCD, so its K and V are fetched
      * into that XCD's L2 once rather than into every XCD's */
     const int tix = xcd_tile(blockIdx.x, a.T);
     if (tix >= a.T) return;                 /* uniform per workgroup, before any barrier */
     const int bh = tix / a.nqb;
-    const int q0 = (tix % a.nqb) * 128 + wave * 32;
+    const int q0 = (tix % a.nqb) * (32 * QW) + wave * 32;
     const uint16_t *Qh = a.q + (size_t)bh * a.Nq * 64;
     const uint16_t *Kh = a.k + (size_t)bh * a.Nk * 64;
     const uint16_t *Vh = a.v + (size_t)bh * a.Nk * 64;
@@ -217,21 +221,23 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
         for (int ds = 0; ds < 4; ds++) qf[ds] = ld_h8(Qh + (size_t)qi * 64 + 16 * ds + 8 * g);
     }
 
-    /* tile staging by LDS DMA: instruction i of wave w (of this half) fills the 16 B slots
-     * p = 256 i + 64 w + lane of a K or V tile (key row p / 8, stored chunk p % 8), so each
-     * lane fetches the global chunk that the swizzle places there: K stores logical chunk c
-     * of row r at c ^ ((r >> 1) & 7), V at c ^ (((r >> 1) & 1) << 2). Keys past Nk re-read
-     * the last key (their probabilities are exactly zero). */
+    /* tile staging by LDS DMA: a tile is 512 slots of 16 B (key row p / 8, stored chunk p % 8)
+     * in 8 blocks of 64; instruction i of wave w (of this half) fills block cb = QW i + w
+     * (slots p = 64 cb + lane), so each lane fetches the global chunk that the swizzle places
+     * there: K stores logical chunk c of row r at c ^ ((r >> 1) & 7), V at
+     * c ^ (((r >> 1) & 1) << 2). Keys past Nk re-read the last key (their probabilities are
+     * exactly zero). */
     typedef __attribute__((address_space(3))) void lds_void_t;
-    const int wv = wave & 3;
     auto dma = [&](int kt0, uint16_t *Kd, uint16_t *Vd) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int p = 256 * i + 64 * wv + lane, r = p >> 3, cp = p & 7;
+        for (int i = 0; i < (8 + QW - 1) / QW; i++) {
+            const int cb = QW * i + wave;
+            if (8 % QW != 0 && cb >= 8) break;   /* uniform per wave */
+            const int p = 64 * cb + lane, r = p >> 3, cp = p & 7;
             const size_t row = (size_t)min(kt0 + r, a.Nk - 1) * 64;
             const int ck = cp ^ ((r >> 1) & 7), cv = cp ^ (((r >> 1) & 1) << 2);
-            __builtin_amdgcn_global_load_lds(Kh + row + 8 * ck, (lds_void_t *)(Kd + (256 * i + 64 * wv) * 8), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(Vh + row + 8 * cv, (lds_void_t *)(Vd + (256 * i + 64 * wv) * 8), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Kh + row + 8 * ck, (lds_void_t *)(Kd + 64 * cb * 8), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Vh + row + 8 * cv, (lds_void_t *)(Vd + 64 * cb * 8), 16, 0, 0);
         }
     };
     /* the DMA writes into LDS complete on vmcnt; each wave waits for its own before the
@@ -376,7 +382,7 @@ __global__ __launch_bounds__(256 * KS) __attribute__((amdgpu_waves_per_eu(4))) v
         /* merge: the second half hands (O, l, m) to the first through LDS (the tile buffers
          * are free after the last trip's barrier): per wave 64 lanes x 16 floats of each O
          * block in Kb0s / Kb1s, l and m in Vb0s (each object holds 4 x 16 x 64 floats) */
-        static_assert(KS * KT * 64 * 2 >= 4 * 16 * 64 * 4, "merge exchange fits a tile buffer");
+        static_assert(KS * KT * 64 * 2 >= QW * 16 * 64 * 4, "merge exchange fits a tile buffer");
         float *X0 = reinterpret_cast<float *>(Kb0s) + wave * 16 * 64 + lane;
         float *X1 = reinterpret_cast<float *>(Kb1s) + wave * 16 * 64 + lane;
         float *X2 = reinterpret_cast<float *>(Vb0s) + wave * 2 * 64 + lane;
@@ -430,14 +436,23 @@ extern "C" hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, co
     AttnArgs a;
     a.q = q; a.k = k; a.v = v; a.o = o; a.H = H; a.Nq = Nq; a.Nk = Nk; a.o_f16 = o_f16;
     a.scale_log2 = 0.125f * ARIA_LOG2E;
-    a.nqb = (Nq + 127) / 128;
+    /* split the keys inside the workgroup when there are enough tiles for both halves
+     * (S = 1296 self-attention: 21 tiles); short key sets (the 256 cross keys) run one half.
+     * Query waves per half: 4 for the split form (two 8-wave workgroups per CU; 3 waves, 448
+     * blocks of 96 instead of 352 of 128 at S = 1296, measured 10 % slower), else the fewest
+     * query slots on the busiest CU (ceil(T / 256) blocks of 32 QW queries), ties to 4: the
+     * cross attention at S = 1296, 32 heads takes 3 (10.6 -> 10.4 us) */
+    const bool split = (Nk + KT - 1) / KT >= 8;
+    int qw = 4;
+    if (!split) {
+        const long t4 = (long)((Nq + 127) / 128) * BH, t3 = (long)((Nq + 95) / 96) * BH;
+        if ((t3 + 255) / 256 * 3 < (t4 + 255) / 256 * 4) qw = 3;
+    }
+    a.nqb = (Nq + 32 * qw - 1) / (32 * qw);
     a.T = a.nqb * BH;
     const dim3 grid((a.T + 7) / 8 * 8);
-    /* split the keys inside the workgroup when there are enough tiles for both halves
-     * (S = 1296 self-attention: 21 tiles); short key sets (the 256 cross keys) run 4 waves */
-    if ((Nk + KT - 1) / KT >= 8)
-        hipLaunchKernelGGL(k_flash_attn<2>, grid, dim3(512), 0, s, a);
-    else
-        hipLaunchKernelGGL(k_flash_attn<1>, grid, dim3(256), 0, s, a);
+    if (split) hipLaunchKernelGGL((k_flash_attn<2, 4>), grid, dim3(512), 0, s, a);
+    else if (qw == 3) hipLaunchKernelGGL((k_flash_attn<1, 3>), grid, dim3(192), 0, s, a);
+    else hipLaunchKernelGGL((k_flash_attn<1, 4>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
