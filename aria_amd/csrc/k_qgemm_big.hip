@@ -137,8 +137,8 @@ struct Stage {
 /* One tile per workgroup; MINB workgroups per CU (MINB = 2 when the tile's registers and
  * LDS allow two: the second workgroup's waves cover one workgroup's barrier waits and its
  * epilogue). The tiles of an XCD are a contiguous run in M-major order (xcd_tile). */
-template <int WT, int FM, int FN, int MODE, bool GELU, int MINB, int NS, int NST>
-__global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T) {
+template <int WT, int FM, int FN, int MODE, bool GELU, int MINB, int NS, int NST, int KSPL>
+__global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN, int T) {
     using St = Stage<WT, FM, FN>;   /* one 64-deep sub-tile; a pipeline stage holds NS of them */
     constexpr int SB = NS * St::BYTES;                                 /* stage bytes */
     constexpr int PD = NST - 1;                                        /* prefetch distance */
@@ -147,14 +147,21 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
     constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
     constexpr int EPI_WAVE = 32 * EPI_STRIDE;                          /* bytes per wave */
     static_assert(NST * SB >= 4 * EPI_WAVE, "the epilogue staging fits the stages");
-    static_assert(NST * SB <= (MINB == 1 ? 160 : 80) * 1024, "the stages fit the LDS");
-    __shared__ __attribute__((aligned(16))) uint8_t smem[NST * SB];
+    static_assert(KSPL == 1 || KSPL == 2, "one or two K halves");
+    static_assert(KSPL * NST * SB <= (MINB == 1 ? 160 : 80) * 1024, "the stages fit the LDS");
+    static_assert(KSPL == 1 || NST * SB >= FM * FN * 16 * 256 * 4, "the second half's partial sums fit its stages");
+    __shared__ __attribute__((aligned(16))) uint8_t smem_all[KSPL * NST * SB];
 
     const int t = xcd_tile(blockIdx.x, T);
     if (t >= T) return;                     /* uniform per workgroup, before any barrier */
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    /* KSPL = 2: waves 4-7 run the second half of the K range on their own pipeline stages, and
+     * their partial sums join the first half's before the epilogue (fixed order) */
+    const int khalf = KSPL == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+    uint8_t *const smem = smem_all + khalf * (NST * SB);
+    const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
     const int lrow = lane & 31, lh = lane >> 5;
-    const int KT = a.K / (St::KK * NS);     /* pipeline steps */
+    const int KT = a.K / (St::KK * NS * KSPL);   /* pipeline steps of this half (host: divisible) */
+    const int kofs = khalf * KT;                 /* this half's first step */
     uint32_t magic = 0x64006400u;           /* fp16 1024 in both halves, kept in a VGPR */
     asm volatile("" : "+v"(magic));
     const uint32_t sbase = (uint32_t)(uintptr_t)smem;
@@ -199,7 +206,7 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
     auto issue = [&](int B, int kt) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < NS; u++) {
-            const int k64 = NS * kt + u;
+            const int k64 = NS * (kt + kofs) + u;
             const uint32_t st = sbase + B * SB + u * St::BYTES;
             if constexpr (WT == ARIA_WI8) {   /* 128 int8 k per K-tile: 128 bytes of every row */
 #pragma unroll
@@ -381,6 +388,29 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
     static_for<NST - 1>([&](auto PP) __attribute__((always_inline)) {
         if (kt + decltype(PP)::value < KT) step(PP, kt + decltype(PP)::value);
     });
+    if constexpr (KSPL == 2) {
+        /* every wave is past its last fragment read (the last step's barrier): the second half
+         * leaves its partial sums in its own stages (lane-major, conflict-free), the first half
+         * adds them to its own (acc_first + acc_second, for every element alike) */
+        using ElT = typename std::conditional<WT == ARIA_WI8, int, float>::type;
+        ElT *X = reinterpret_cast<ElT *>(smem_all + NST * SB) + tid;
+        if (khalf == 1) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) X[((i * FN + j) * 16 + r) * 256] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (khalf == 1) return;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = acc[i][j][r] + X[((i * FN + j) * 16 + r) * 256];
+    }
     /* every wave is past its last fragment read (the last step's barrier): the stages hold the
      * epilogue staging */
     float *E = reinterpret_cast<float *>(smem + wave * EPI_WAVE);
@@ -388,40 +418,41 @@ __global__ __launch_bounds__(256, MINB) void k_qgemm_big(QArgs a, int NTN, int T
 }
 
 /* NST = 0: three stages where they fit the LDS share of MINB workgroups, else two */
-template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int NS = 1, int NST = 0>
+template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int KSPL = 1, int NS = 1, int NST = 0>
 static void launch_big_m(const QArgs &a, hipStream_t s) {
     constexpr int BM = 32 * FM, BN = 128 * FN;
-    constexpr int NSTA = NST ? NST : (3 * NS * Stage<WT, FM, FN>::BYTES <= (MINB == 1 ? 160 : 80) * 1024 ? 3 : 2);
+    constexpr int NSTA = NST ? NST : (3 * KSPL * NS * Stage<WT, FM, FN>::BYTES <= (MINB == 1 ? 160 : 80) * 1024 ? 3 : 2);
     const int MT = (a.M + BM - 1) / BM, NTN = (a.N + BN - 1) / BN, T = MT * NTN;
     const int grid = ((T + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_qgemm_big<WT, FM, FN, MODE, GELU, MINB, NS, NSTA>), dim3(grid), dim3(256), 0, s, a, NTN, T);
+    hipLaunchKernelGGL((k_qgemm_big<WT, FM, FN, MODE, GELU, MINB, NS, NSTA, KSPL>), dim3(grid), dim3(256 * KSPL), 0, s,
+                       a, NTN, T);
 }
 
 /* one kernel per fused epilogue mode (a run-time mode switch inside the store loop makes
  * every store wait for the loads of the modes that read); HEADS needs FN = 2 (a head's 64
  * columns in one wave) */
-template <int WT, int FM, int FN, int MINB>
+template <int WT, int FM, int FN, int MINB, int KSPL = 1>
 static void launch_big(const QArgs &a, hipStream_t s) {
     switch (a.epi.mode) {
-        case ARIA_EPI_GATE_RES: launch_big_m<WT, FM, FN, ARIA_EPI_GATE_RES, false, MINB>(a, s); break;
-        case ARIA_EPI_ADD: launch_big_m<WT, FM, FN, ARIA_EPI_ADD, false, MINB>(a, s); break;
+        case ARIA_EPI_GATE_RES: launch_big_m<WT, FM, FN, ARIA_EPI_GATE_RES, false, MINB, KSPL>(a, s); break;
+        case ARIA_EPI_ADD: launch_big_m<WT, FM, FN, ARIA_EPI_ADD, false, MINB, KSPL>(a, s); break;
         case ARIA_EPI_ADD_DYT:
-            if constexpr (WT == ARIA_WF16) launch_big_m<WT, FM, FN, ARIA_EPI_ADD_DYT, false, MINB>(a, s);
+            if constexpr (WT == ARIA_WF16) launch_big_m<WT, FM, FN, ARIA_EPI_ADD_DYT, false, MINB, KSPL>(a, s);
             break;
         case ARIA_EPI_HEADS:
-            if constexpr (FN >= 2) launch_big_m<WT, FM, FN, ARIA_EPI_HEADS, false, MINB>(a, s);
+            if constexpr (FN >= 2) launch_big_m<WT, FM, FN, ARIA_EPI_HEADS, false, MINB, KSPL>(a, s);
             break;
-        case ARIA_EPI_GLU: launch_big_m<WT, FM, FN, ARIA_EPI_GLU, false, MINB>(a, s); break;
+        case ARIA_EPI_GLU: launch_big_m<WT, FM, FN, ARIA_EPI_GLU, false, MINB, KSPL>(a, s); break;
         default:
-            if (a.gelu) launch_big_m<WT, FM, FN, ARIA_EPI_STORE, true, MINB>(a, s);
-            else launch_big_m<WT, FM, FN, ARIA_EPI_STORE, false, MINB>(a, s);
+            if (a.gelu) launch_big_m<WT, FM, FN, ARIA_EPI_STORE, true, MINB, KSPL>(a, s);
+            else launch_big_m<WT, FM, FN, ARIA_EPI_STORE, false, MINB, KSPL>(a, s);
             break;
     }
 }
 
-/* the configurations compiled (FM, FN, workgroups per CU), index = the cfg argument; measured
- * at M = 2592 (DiT shapes), fp16 activations:
- *   0: 96 x 128, two per CU: N <= 1024 (sa_out, ca_out, ff_out; K = 1024 and 4096)
+/* the configurations compiled (FM, FN, workgroups per CU, K halves), index = the cfg argument;
+ * measured at M = 2592 (DiT shapes), fp16 activations:
+ *   0: 96 x 128, two per CU: N <= 1024 with an odd number of K-tiles
  *   1: 128 x 128, two per CU: N = 3072 without HEADS
  *   2: 64 x 256, two per CU: the HEADS projections (qkv N = 3072, ca_q N = 1024): a head's 64
  *      columns in one wave, and the second workgroup per CU covers the other's HEADS epilogue
@@ -430,11 +461,15 @@ static void launch_big(const QArgs &a, hipStream_t s) {
  *      once; Q8 36.5 -> 33.3 us, Q4 38.2 -> 36.0 us against the weights-in-registers kernel)
  *   4: 224 x 128, two per CU in two stages: N > 4096 (the GLU ff_in, N = 8192: Q8 74.4 ->
  *      58.3 us, Q4 73.4 -> 63.5 us)
+ *   5: 96 x 128 in 8-wave workgroups, one per CU, waves 4-7 on the second half of the K range:
+ *      N <= 1024 (sa_out, ca_out, ff_out: 216 tiles leave 40 CUs idle, and the split gives the
+ *      busy ones two waves per SIMD; ff_out Q4 42.8 -> 38.6 us, Q8 36.4 -> 33.3 us)
  * Larger FM amortises each unpacked weight over more rows; 96 x 256, 64 x 128 and 192 x 256
  * (one per CU) measured slower at every DiT shape. */
-#define BIG_CFGS(X) X(0, 3, 1, 2) X(1, 4, 1, 2) X(2, 2, 2, 2) X(3, 6, 1, 2) X(4, 7, 1, 2)
-static const int big_fm[] = {3, 4, 2, 6, 7};
-static const int big_fn[] = {1, 1, 2, 1, 1};
+#define BIG_CFGS(X) X(0, 3, 1, 2, 1) X(1, 4, 1, 2, 1) X(2, 2, 2, 2, 1) X(3, 6, 1, 2, 1) X(4, 7, 1, 2, 1) X(5, 3, 1, 1, 2)
+static const int big_fm[] = {3, 4, 2, 6, 7, 3};
+static const int big_fn[] = {1, 1, 2, 1, 1, 1};
+static const int big_ks[] = {1, 1, 1, 1, 1, 2};   /* 2: the K range split inside the workgroup */
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
 
@@ -446,7 +481,7 @@ int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
  * a per-row time that falls with BM (each LDS weight fragment feeds more MFMAs). It picks the
  * fastest configuration at all eight shapes; against the LDS-operand kernel's 192 x 128
  * tiles: 105.6 -> 97.0 us (N = 3840), 136.7 -> 119.8 us (N = 4608) at M = 11016. */
-#define BIG_F16_CFGS(X) X(0, 2, 1, 2) X(1, 3, 1, 2) X(2, 4, 1, 2) X(3, 5, 1, 2) X(4, 6, 1, 2)
+#define BIG_F16_CFGS(X) X(0, 2, 1, 2, 1) X(1, 3, 1, 2, 1) X(2, 4, 1, 2, 1) X(3, 5, 1, 2, 1) X(4, 6, 1, 2, 1)
 static const int big_f16_fn[] = {1, 1, 1, 1, 1};
 
 int qgemm_big_f16_pick(int M, int N) {
@@ -466,8 +501,8 @@ static hipError_t qgemm_big_f16_launch(const QArgs &a, int cfg, hipStream_t s) {
     if (cfg < 0 || cfg >= (int)(sizeof big_f16_fn / sizeof big_f16_fn[0]) ||
         (a.epi.mode == ARIA_EPI_HEADS && big_f16_fn[cfg] < 2))
         return hipErrorInvalidValue;
-#define F16_CASE(i, fm, fn, mb) \
-    case i: launch_big<ARIA_WF16, fm, fn, mb>(a, s); break;
+#define F16_CASE(i, fm, fn, mb, ks) \
+    case i: launch_big<ARIA_WF16, fm, fn, mb, ks>(a, s); break;
     switch (cfg) {
         BIG_F16_CFGS(F16_CASE)
         default: return hipErrorInvalidValue;
@@ -481,12 +516,12 @@ int qgemm_big_bn(int cfg) { return 128 * big_fn[cfg]; }
 hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
     if (wt == ARIA_WF16 && a.K % KB == 0 && (!a.gelu || a.epi.mode == ARIA_EPI_STORE)) return qgemm_big_f16_launch(a, cfg, s);
     if (a.K % KB || cfg < 0 || cfg >= qgemm_big_ncfg() || (a.gelu && a.epi.mode != ARIA_EPI_STORE) ||
-        (a.epi.mode == ARIA_EPI_HEADS && big_fn[cfg] < 2))
+        (a.epi.mode == ARIA_EPI_HEADS && big_fn[cfg] < 2) || (a.K / KB) % big_ks[cfg])
         return hipErrorInvalidValue;
-#define BIG_CASE(i, fm, fn, mb)                                          \
+#define BIG_CASE(i, fm, fn, mb, ks)                                        \
     case i:                                                              \
-        if (wt == ARIA_WQ8) launch_big<ARIA_WQ8, fm, fn, mb>(a, s);      \
-        else launch_big<ARIA_WQ4, fm, fn, mb>(a, s);                     \
+        if (wt == ARIA_WQ8) launch_big<ARIA_WQ8, fm, fn, mb, ks>(a, s);  \
+        else launch_big<ARIA_WQ4, fm, fn, mb, ks>(a, s);                 \
         break;
     if (wt != ARIA_WQ8 && wt != ARIA_WQ4) return hipErrorInvalidValue;
     switch (cfg) {
@@ -505,16 +540,18 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
  *   2: 128 x 128, two per CU in two stages: 1024 < N <= 3072 (N = 3072: 19.5 -> 17.6 us
  *      against 128 x 256 one per CU)
  *   3: 192 x 128, two per CU in two stages: N > 3072 (ff_in N = 4096: 29.3 -> 22.7 us;
- *      the GLU ff_in N = 8192: 61.4 -> 49.6 us) */
-#define BIG_I8_CFGS(X) X(0, 2, 1, 2) X(1, 2, 2, 2) X(2, 4, 1, 2) X(3, 6, 1, 2)
-int qgemm_big_i8_ncfg() { return 4; }
+ *      the GLU ff_in N = 8192: 61.4 -> 49.6 us)
+ *   4: 96 x 128 in 8-wave workgroups (the K range split, two stages each): N <= 1024 with
+ *      K >= 2048 (ff_out: 23.6 -> 21.7 us) */
+#define BIG_I8_CFGS(X) X(0, 2, 1, 2, 1) X(1, 2, 2, 2, 1) X(2, 4, 1, 2, 1) X(3, 6, 1, 2, 1) X(4, 3, 1, 1, 2)
+int qgemm_big_i8_ncfg() { return 5; }
 
 hipError_t qgemm_big_i8_launch(const QArgs &a, int cfg, hipStream_t s) {
     if (a.K % 128 || (a.gelu && a.epi.mode != ARIA_EPI_STORE)) return hipErrorInvalidValue;
-#define BIG_I8_CASE(i, fm, fn, mb)                                                         \
+#define BIG_I8_CASE(i, fm, fn, mb, ks)                                                       \
     case i:                                                                                \
-        if (a.epi.mode == ARIA_EPI_HEADS && fn < 2) return hipErrorInvalidValue;           \
-        launch_big<ARIA_WI8, fm, fn, mb>(a, s);                                            \
+        if ((a.epi.mode == ARIA_EPI_HEADS && fn < 2) || (a.K / 128) % ks) return hipErrorInvalidValue; \
+        launch_big<ARIA_WI8, fm, fn, mb, ks>(a, s);                                        \
         break;
     switch (cfg) {
         BIG_I8_CFGS(BIG_I8_CASE)
