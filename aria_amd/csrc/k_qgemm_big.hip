@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
     static_assert(NST * SB >= 4 * EPI_WAVE, "the epilogue staging fits the stages");
     static_assert(KSPL == 1 || KSPL == 2, "one or two K halves");
     static_assert(KSPL * NST * SB <= (MINB == 1 ? 160 : 80) * 1024, "the stages fit the LDS");
-    static_assert(KSPL == 1 || NST * SB >= FM * FN * 16 * 256 * 4, "the second half's partial sums fit its stages");
+    static_assert(KSPL == 1 || KSPL * NST * SB >= FM * FN * 16 * 256 * 4, "the second half's partial sums fit the stages");
     __shared__ __attribute__((aligned(16))) uint8_t smem_all[KSPL * NST * SB];
 
     const int t = xcd_tile(blockIdx.x, T);
@@ -390,10 +390,12 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
     });
     if constexpr (KSPL == 2) {
         /* every wave is past its last fragment read (the last step's barrier): the second half
-         * leaves its partial sums in its own stages (lane-major, conflict-free), the first half
-         * adds them to its own (acc_first + acc_second, for every element alike) */
+         * leaves its partial sums in the stage memory (lane-major, conflict-free), the first half
+         * adds them to its own (acc_first + acc_second, for every element alike), and a second
+         * barrier keeps the second half's waves until every partial sum has been read, before
+         * the epilogue stages its rows in the same memory */
         using ElT = typename std::conditional<WT == ARIA_WI8, int, float>::type;
-        ElT *X = reinterpret_cast<ElT *>(smem_all + NST * SB) + tid;
+        ElT *X = reinterpret_cast<ElT *>(smem_all) + tid;
         if (khalf == 1) {
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -403,13 +405,16 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
                     for (int r = 0; r < 16; r++) X[((i * FN + j) * 16 + r) * 256] = acc[i][j][r];
         }
         __syncthreads();
+        if (khalf == 0) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = acc[i][j][r] + X[((i * FN + j) * 16 + r) * 256];
+        }
+        __syncthreads();
         if (khalf == 1) return;
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[i][j][r] = acc[i][j][r] + X[((i * FN + j) * 16 + r) * 256];
     }
     /* every wave is past its last fragment read (the last step's barrier): the stages hold the
      * epilogue staging */
@@ -469,7 +474,7 @@ static void launch_big(const QArgs &a, hipStream_t s) {
 #define BIG_CFGS(X) X(0, 3, 1, 2, 1) X(1, 4, 1, 2, 1) X(2, 2, 2, 2, 1) X(3, 6, 1, 2, 1) X(4, 7, 1, 2, 1) X(5, 3, 1, 1, 2)
 static const int big_fm[] = {3, 4, 2, 6, 7, 3};
 static const int big_fn[] = {1, 1, 2, 1, 1, 1};
-static const int big_ks[] = {1, 1, 1, 1, 1, 2};   /* 2: the K range split inside the workgroup */
+static const int big_ks[] = {1, 1, 1, 1, 1, 2};   /* 2: the K range split inside the workgroup */   /* 2: the K range split inside the workgroup */
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
 
