@@ -506,8 +506,11 @@ static hipError_t qgemm_big_f16_launch(const QArgs &a, int cfg, hipStream_t s) {
     if (cfg < 0 || cfg >= (int)(sizeof big_f16_fn / sizeof big_f16_fn[0]) ||
         (a.epi.mode == ARIA_EPI_HEADS && big_f16_fn[cfg] < 2))
         return hipErrorInvalidValue;
-#define F16_CASE(i, fm, fn, mb, ks) \
-    case i: launch_big<ARIA_WF16, fm, fn, mb, ks>(a, s); break;
+#define F16_CASE(i, fm, fn, mb, ks)                                \
+    case i:                                                        \
+        if ((a.K / KB) % ks) return hipErrorInvalidValue;          \
+        launch_big<ARIA_WF16, fm, fn, mb, ks>(a, s);               \
+        break;
     switch (cfg) {
         BIG_F16_CFGS(F16_CASE)
         default: return hipErrorInvalidValue;
