@@ -542,6 +542,8 @@ struct aria_cuda_dit {
     /* the step as a HIP graph (see graph_ensure) */
     int gstate;                             /* GRAPH_NONE / GRAPH_LIVE / GRAPH_OFF */
     int no_graph;                           /* ARIA_NO_GRAPH at create: inline for good */
+    int graph_fail;                         /* ARIA_GRAPH_FAIL at create: every capture is
+                                               treated as failed (tests the fallback) */
     hipGraph_t graph;
     hipGraphExec_t gexec;
     /* sampler staging (see aria_cuda_dit_sample) */
@@ -638,6 +640,8 @@ aria_cuda_dit *aria_hip_dit_create_ex(const aria_sa3_dit_view *v, aria_dtype pre
     h->n_mem = v->n_mem; h->rot = v->rot_dim;
     const char *ng = getenv("ARIA_NO_GRAPH");   /* read once per handle */
     h->no_graph = ng && ng[0] && ng[0] != '0';
+    const char *gf = getenv("ARIA_GRAPH_FAIL");
+    h->graph_fail = gf && gf[0] && gf[0] != '0';
     h->gstate = h->no_graph ? GRAPH_OFF : GRAPH_NONE;
     if (hipStreamCreateWithFlags(&h->st, hipStreamNonBlocking) != hipSuccess) { free(h); return NULL; }
     /* VRAM fit: packed blocks (<= fp16 size) + fp32 io projections, with margin */
@@ -857,7 +861,9 @@ static int step_compute(aria_cuda_dit *h, hipStream_t s) {
  * on the current request's buffers and replayed from then on; set_request (for a new layout)
  * and an overlay load drop it. Capture is thread-local, so work that other threads enqueue
  * meanwhile is not pulled in. If capture or instantiation fails the handle runs the kernels
- * inline from then on, with the same results. Returns 1 when a graph is ready. */
+ * inline from then on, with the same results (the captured work never ran, so the step is
+ * enqueued again inline). ARIA_GRAPH_FAIL set at create takes the failure branch after every
+ * capture, which lets a test reach it. Returns 1 when a graph is ready. */
 static int graph_ensure(aria_cuda_dit *h) {
     if (h->gstate != GRAPH_NONE) return h->gstate == GRAPH_LIVE;
     h->gstate = GRAPH_OFF;   /* unless everything below succeeds */
@@ -870,7 +876,7 @@ static int graph_ensure(aria_cuda_dit *h) {
     hipGraph_t g = NULL;
     hipGraphExec_t x = NULL;
     const hipError_t ec = hipStreamEndCapture(h->st, &g);
-    if (rc || ec != hipSuccess || !g || hipGraphInstantiate(&x, g, NULL, NULL, 0) != hipSuccess) {
+    if (rc || ec != hipSuccess || !g || h->graph_fail || hipGraphInstantiate(&x, g, NULL, NULL, 0) != hipSuccess) {
         hipGetLastError();
         if (g) hipGraphDestroy(g);
         return 0;

@@ -208,6 +208,40 @@ def test_dit_graph_matches_inline(hip, port, monkeypatch):
     inline.free(); graph.free()
 
 
+def test_dit_graph_capture_failure_falls_back(hip, port, monkeypatch):
+    """A capture that fails (forced by ARIA_GRAPH_FAIL at create: the failure branch drops the
+    captured graph, whose work never ran) leaves the handle on inline launches for good, with
+    results bit-identical to ARIA_NO_GRAPH, over repeated steps and a new request."""
+    M = model(52)
+    T, n_cond, H, rot = 30, 8, 2, 32
+    io_ch, ed = M["project_in"].shape[1], M["project_in"].shape[0]
+    S = M["memory_tokens"].shape[0] + T
+    c, s = port.rope_freqs(S, rot, 10000.0)
+    _, ced, _ = inputs(9, 2, io_ch, T, n_cond, ed)
+    monkeypatch.setenv("ARIA_NO_GRAPH", "1")
+    inline = make_dit(M, 4, H, rot)
+    monkeypatch.delenv("ARIA_NO_GRAPH")
+    monkeypatch.setenv("ARIA_GRAPH_FAIL", "1")
+    failing = make_dit(M, 4, H, rot)
+    monkeypatch.delenv("ARIA_GRAPH_FAIL")
+    for d in (inline, failing):
+        d.set_request(T, [ced[0], ced[1]], c, s)
+    for k in range(3):
+        x, _, g = inputs(400 + k, 2, io_ch, T, n_cond, ed)
+        a, b = inline.step(x, g), failing.step(x, g)
+        assert not failing.graph_active
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {k} differs from inline"
+    T2 = 22
+    S2 = M["memory_tokens"].shape[0] + T2
+    c2, s2 = port.rope_freqs(S2, rot, 10000.0)
+    for d in (inline, failing):
+        d.set_request(T2, [ced[0]], c2, s2)
+    x, _, g = inputs(410, 1, io_ch, T2, n_cond, ed)
+    assert np.array_equal(inline.step(x, g).view(np.uint32), failing.step(x, g).view(np.uint32))
+    assert not failing.graph_active
+    inline.free(); failing.free()
+
+
 def test_dit_device_buffers_run(hip, port):
     """aria_hip_dit_device_buffers + aria_hip_dit_run: the step on HBM-resident buffers equals
     the host-buffer step bit for bit."""
