@@ -52,7 +52,7 @@ def _rms_rel(got, ref):
 def test_dec_matches_reference_decoder(model, T):
     """odd T pads one frame (src/aria_sa3_dec.c:67); T = 1 leaves the shifted pass one chunk of
     halo plus data; T = 108 and 646 are the 10 s and 60 s clips bench.py times; T = 1100 (17600
-    output rows) runs the mapping GEMM's 128 x 128 tiles"""
+    output rows) is the longest checked against the reference"""
     rd, dv, _ = model
     lat = rng(100 + T).standard_normal((256, T)).astype(np.float32)
     print(f"[gpu] decoder T={T}", flush=True)
