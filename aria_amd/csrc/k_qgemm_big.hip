@@ -389,32 +389,42 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
         if (kt + decltype(PP)::value < KT) step(PP, kt + decltype(PP)::value);
     });
     if constexpr (KSPL == 2) {
-        /* every wave is past its last fragment read (the last step's barrier): the second half
-         * leaves its partial sums in the stage memory (lane-major, conflict-free), the first half
-         * adds them to its own (acc_first + acc_second, for every element alike), and a second
-         * barrier keeps the second half's waves until every partial sum has been read, before
-         * the epilogue stages its rows in the same memory */
+        /* every wave is past its last fragment read (the last step's barrier). The halves share
+         * the epilogue: the first finalises row blocks 0 .. F0 - 1, the second the rest, each
+         * taking the other half's partial sums of its blocks through the stage memory
+         * (lane-major, conflict-free). Every element is acc_first + acc_second (an fp32 sum is
+         * the same in either order; int32 exact). The second barrier keeps the partial sums
+         * until both halves have read them, before the epilogue stages rows in that memory. */
+        constexpr int F0 = (FM + 1) / 2;
         using ElT = typename std::conditional<WT == ARIA_WI8, int, float>::type;
         ElT *X = reinterpret_cast<ElT *>(smem_all) + tid;
-        if (khalf == 1) {
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+        for (int i = 0; i < FM; i++)
+            if ((khalf == 1) == (i < F0)) {
 #pragma unroll
                 for (int j = 0; j < FN; j++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) X[((i * FN + j) * 16 + r) * 256] = acc[i][j][r];
-        }
+            }
         __syncthreads();
-        if (khalf == 0) {
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+        for (int i = 0; i < FM; i++)
+            if ((khalf == 0) == (i < F0)) {
 #pragma unroll
                 for (int j = 0; j < FN; j++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) acc[i][j][r] = acc[i][j][r] + X[((i * FN + j) * 16 + r) * 256];
-        }
+            }
         __syncthreads();
-        if (khalf == 1) return;
+        float *E = reinterpret_cast<float *>(smem + wave * EPI_WAVE);
+        if (khalf == 0) {
+            epilogue<F0, FN, WT, MODE, GELU, AccT>(a, *reinterpret_cast<AccT(*)[F0][FN]>(&acc[0]), E, lane, m0,
+                                                   n0 + wave * 32 * FN);
+        } else if constexpr (FM > F0) {
+            epilogue<FM - F0, FN, WT, MODE, GELU, AccT>(a, *reinterpret_cast<AccT(*)[FM - F0][FN]>(&acc[F0]), E, lane,
+                                                        m0 + 32 * F0, n0 + wave * 32 * FN);
+        }
+        return;
     }
     /* every wave is past its last fragment read (the last step's barrier): the stages hold the
      * epilogue staging */
