@@ -68,6 +68,9 @@ def parse():
     ap.add_argument("--pmc-gemm", action="store_true",
                     help="for rocprofv3 --pmc: the config-3 GEMMs (5 launches each) and two forwards of each "
                          "config-4 block variant, untimed")
+    ap.add_argument("--micro", action="store_true",
+                    help="only the issue-rate and bandwidth probes (k_micro.hip): fp16 MFMA, fp32 FMA, exp2, "
+                         "reciprocal, LDS and L1 reads")
     ap.add_argument("--vendor", action="store_true",
                     help="only the vendor-library reference points: PyTorch's fp16 GEMM (hipBLASLt) and "
                          "scaled_dot_product_attention at this build's GEMM and attention shapes")
@@ -269,6 +272,9 @@ def main():
     print(f"[bench] device: {aria_amd.device_info()}", file=sys.stderr, flush=True)
 
     rng = np.random.default_rng(SEED)
+    if args.micro:
+        print(json.dumps({"micro": micro_leg(L, chk, DeviceArray, Timer, stream)}), flush=True)
+        return
     if args.pmc_gemm:
         def run_only(fn, reps):
             for i in range(reps):
@@ -448,6 +454,52 @@ def main():
         "wall_s_timed": round(t_wall, 3),
     }
     print(json.dumps(line), flush=True)
+
+
+def micro_leg(L, chk, DeviceArray, Timer, stream):
+    """The issue rates and bandwidths the kernel designs lean on (k_micro.hip), each the fastest
+    of 5 timed launches after 2 untimed ones, 1024-2048 workgroups of 256 lanes (4-8 waves per
+    SIMD, every CU busy). The clock under load is not read from the driver: a 32x32x16 fp16 MFMA
+    keeps its SIMD's matrix pipe busy 32 cycles, so the MFMA probe's rate per SIMD x 32 is the
+    effective clock, and the other probes are expressed in cycles of that clock (per wave64
+    instruction per SIMD; bytes per clock per CU). SIMDs = 1024 (256 CUs x 4)."""
+    simds, cus = 1024, 256
+    def run(which, grid, iters):
+        out = DeviceArray(grid * 256)
+        tab = DeviceArray(grid * 4096) if which == 5 else None
+        f = lambda: L.aria_hip_micro_dev(which, grid, iters, out.p, tab.p if tab else None, stream)
+        for _ in range(2):
+            chk(f())
+        chk(L.aria_hip_stream_sync(stream))
+        best = 1e30
+        for _ in range(5):
+            tm = Timer(stream)
+            tm.start()
+            chk(f())
+            best = min(best, tm.stop())
+        out.free()
+        if tab:
+            tab.free()
+        return best * 1e-3   # seconds
+    res = {}
+    g, it = 1024, 4000
+    t = run(0, g, it)
+    mfma = g * 4 * it * 4                       # MFMA instructions
+    flops = mfma * 32 * 32 * 16 * 2
+    clk = mfma / simds * 32 / t                 # effective clock (Hz)
+    res["mfma_f16_32x32x16"] = {"TFLOP/s": round(flops / t / 1e12, 1), "frac_of_2500": round(flops / t / 2.5e15, 3),
+                                "effective_clock_GHz": round(clk / 1e9, 3)}
+    for which, name in ((1, "v_fma_f32"), (2, "v_exp_f32"), (3, "v_rcp_f32")):
+        g, it = 2048, 4000
+        t = run(which, g, it)
+        instr = g * 4 * it * 8                  # wave64 instructions
+        res[name] = {"cycles_per_wave_instr_per_simd": round(clk * t / (instr / simds), 2)}
+    for which, name in ((4, "ds_read_b128"), (5, "global_load_dwordx4_l1")):
+        g, it = 1024, 2000
+        t = run(which, g, it)
+        byt = g * 4 * it * 8 * 64 * 16
+        res[name] = {"bytes_per_clk_per_cu": round(byt / t / clk / cus, 1), "TB/s": round(byt / t / 1e12, 1)}
+    return res
 
 
 def ceiling_leg(L, chk, DeviceArray, time_loop, stream, reps):
