@@ -94,14 +94,26 @@ __device__ __forceinline__ float epi_elem(float n, float xv, float sc, float sh)
     return n;
 }
 
-/* register-resident fast path: dim == VPL * 4 * LPR */
+/* register-resident fast path: dim == VPL * 4 * LPR.
+ * With a full wave per row (LPR = 64) and two or more broadcast vectors (gain, bias, scale,
+ * shift), the workgroup's four rows share them: the 256 lanes load each vector once into LDS
+ * (forming scale + scale_add and shift + shift_add there, once), and every wave reads its lanes'
+ * parts back from LDS. Per row that replaces 8-20 KB of L1 requests by one LDS read of the same
+ * bytes (a CU reads 3x more per clock from LDS than from L1). A workgroup whose rows straddle
+ * two batches of the modulation loads per lane as before. */
 template <int NORM, int VPL, int LPR, int EPI>
 __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
     constexpr int RPW = ARIA_WAVE / LPR;
+    constexpr int NVEC = ((EPI & EPI_W) ? 1 : 0) + ((EPI & EPI_B) ? 1 : 0) + ((EPI & EPI_MOD) ? 2 : 0);
+    constexpr bool SHARE = LPR == 64 && NVEC >= 2;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
+    const int row0 = (blockIdx.x * 4 + wave) * RPW + lane / LPR;
     const int l = lane % LPR;
-    if (row >= a.rows) return;   /* whole LPR-lane groups leave together */
+    if (!SHARE && row0 >= a.rows) return;   /* whole LPR-lane groups leave together */
+    /* SHARE: every wave stays to the barrier; a row past the end re-reads the last row and
+     * stores nothing */
+    const bool live = row0 < a.rows;
+    const int row = live ? row0 : a.rows - 1;
     const int dim = a.dim;
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x + (size_t)row * dim);
     float4 v[VPL];
@@ -114,32 +126,51 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
     const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 wv[VPL], bv[VPL], scv[VPL], shv[VPL];
-    {
-        const float4 *sc4 = nullptr, *sh4 = nullptr, *sca4 = nullptr, *sha4 = nullptr;
+    /* the vectors of batch bt at float4 column c4 */
+    auto vecs_at = [&](int bt, int c4, float4 &w, float4 &b, float4 &sc, float4 &sh) __attribute__((always_inline)) {
+        w = (EPI & EPI_W) ? w4[c4] : z4;
+        b = (EPI & EPI_B) ? b4[c4] : z4;
+        sc = z4; sh = z4;
         if (EPI & EPI_MOD) {
-            const int bt = row / a.rows_per_batch;
-            sc4 = reinterpret_cast<const float4 *>(a.scale + (size_t)bt * a.mod_bs);
-            sh4 = reinterpret_cast<const float4 *>(a.shift + (size_t)bt * a.mod_bs);
+            sc = reinterpret_cast<const float4 *>(a.scale + (size_t)bt * a.mod_bs)[c4];
+            sh = reinterpret_cast<const float4 *>(a.shift + (size_t)bt * a.mod_bs)[c4];
             if (EPI & EPI_MADD) {
-                sca4 = reinterpret_cast<const float4 *>(a.scale_add + (size_t)bt * a.add_bs);
-                sha4 = reinterpret_cast<const float4 *>(a.shift_add + (size_t)bt * a.add_bs);
+                const float4 sa = reinterpret_cast<const float4 *>(a.scale_add + (size_t)bt * a.add_bs)[c4];
+                const float4 ha = reinterpret_cast<const float4 *>(a.shift_add + (size_t)bt * a.add_bs)[c4];
+                sc = make_float4(sc.x + sa.x, sc.y + sa.y, sc.z + sa.z, sc.w + sa.w);
+                sh = make_float4(sh.x + ha.x, sh.y + ha.y, sh.z + ha.z, sh.w + ha.w);
             }
         }
+    };
+    bool shared_done = false;
+    if constexpr (SHARE) {
+        /* one batch for the whole workgroup? (uniform per workgroup) */
+        const int rf = blockIdx.x * 4, rl = min(rf + 3, a.rows - 1);
+        const bool one = !(EPI & EPI_MOD) || rf / a.rows_per_batch == rl / a.rows_per_batch;
+        if (one) {
+            __shared__ float4 sv[4][VPL * 64];
+            const int bt = rf / a.rows_per_batch;
+            for (int c4 = threadIdx.x; c4 < VPL * 64; c4 += 256) {
+                float4 w, b, sc, sh;
+                vecs_at(bt, c4, w, b, sc, sh);
+                sv[0][c4] = w; sv[1][c4] = b; sv[2][c4] = sc; sv[3][c4] = sh;
+            }
+            __syncthreads();
 #pragma unroll
-        for (int j = 0; j < VPL; j++) {
-            const int c4 = j * LPR + l;
-            wv[j] = (EPI & EPI_W) ? w4[c4] : z4;
-            bv[j] = (EPI & EPI_B) ? b4[c4] : z4;
-            scv[j] = z4; shv[j] = z4;
-            if (EPI & EPI_MOD) {
-                scv[j] = sc4[c4]; shv[j] = sh4[c4];
-                if (EPI & EPI_MADD) {
-                    const float4 sa = sca4[c4], ha = sha4[c4];
-                    scv[j] = make_float4(scv[j].x + sa.x, scv[j].y + sa.y, scv[j].z + sa.z, scv[j].w + sa.w);
-                    shv[j] = make_float4(shv[j].x + ha.x, shv[j].y + ha.y, shv[j].z + ha.z, shv[j].w + ha.w);
-                }
+            for (int j = 0; j < VPL; j++) {
+                const int c4 = j * 64 + l;
+                wv[j] = (EPI & EPI_W) ? sv[0][c4] : z4;
+                bv[j] = (EPI & EPI_B) ? sv[1][c4] : z4;
+                scv[j] = (EPI & EPI_MOD) ? sv[2][c4] : z4;
+                shv[j] = (EPI & EPI_MOD) ? sv[3][c4] : z4;
             }
+            shared_done = true;
         }
+    }
+    if (!shared_done) {
+        const int bt = (EPI & EPI_MOD) ? row / a.rows_per_batch : 0;
+#pragma unroll
+        for (int j = 0; j < VPL; j++) vecs_at(bt, j * LPR + l, wv[j], bv[j], scv[j], shv[j]);
     }
 
     float inv = 0.0f, mu = 0.0f, rstd = 0.0f;
@@ -183,6 +214,7 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
             mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[j].x), fabsf(v[j].y))), fmaxf(fabsf(v[j].z), fabsf(v[j].w)));
         }
         mx = grp_max<LPR>(mx);
+        if (!live) return;
         const float qinv = mx > 0.0f ? 127.0f / mx : 0.0f;
         uint32_t *yq = reinterpret_cast<uint32_t *>((int8_t *)a.y + (size_t)row * dim);
 #pragma unroll
@@ -190,6 +222,7 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
         if (l == 0) a.sx[row] = mx / 127.0f;
         return;
     }
+    if (!live) return;
 #pragma unroll
     for (int j = 0; j < VPL; j++) {
         const int c4 = j * LPR + l;
