@@ -27,7 +27,7 @@
  * l is accumulated (v_dot2_f32_f16, exact products) from the same fp16 P that multiplies
  * V. The running max is a lazy reference (moved only when a tile exceeds it by 2^8), so
  * the accumulators are rarely rescaled; O / l does not depend on the reference chosen.
- * Workgroup: QW = 3 or 4 waves x 32 queries of one (batch, head), twice the waves when the
+ * Workgroup: QW = 3 to 6 waves x 32 queries of one (batch, head), twice the waves when the
  * keys are split in two halves inside the workgroup (long key sets); K and V tiles
  * of 64 keys are staged key-major in LDS (swizzled, conflict-free) by LDS DMA
  * (global_load_lds_dwordx4, no staging registers), the next tile's transfer running under
@@ -178,7 +178,7 @@ __device__ __forceinline__ uint32_t pack2h_rn(float x, float y) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2_v));
 }
 
-/* QW (3 or 4) waves of 32 queries per key half. KS = 1: all keys. KS = 2: 2 QW waves; waves QW..2 QW - 1
+/* QW (3 to 6) waves of 32 queries per key half. KS = 1: all keys. KS = 2: 2 QW waves; waves QW..2 QW - 1
  * take the second half of the key tiles with their own LDS buffers, and the halves merge
  * (max, row sum, O) through LDS at the end: twice the waves per query block without any
  * exchange between workgroups. Both halves run the same number of loop trips, so every
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(4)
     __shared__ __attribute__((aligned(16))) uint16_t Vb0s[KS * KT * 64];
     __shared__ __attribute__((aligned(16))) uint16_t Vb1s[KS * KT * 64];
 
-    static_assert(QW == 3 || QW == 4, "three or four query waves per key half");
+    static_assert(QW >= 3 && QW <= 6, "three to six query waves per key half");
     /* the wave index in a scalar register: everything derived from it stays scalar */
     const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int half = KS == 1 ? 0 : wid / QW;
@@ -381,11 +381,14 @@ __global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(4)
     if constexpr (KS == 2) {
         /* merge: the second half hands (O, l, m) to the first through LDS (the tile buffers
          * are free after the last trip's barrier): per wave 64 lanes x 16 floats of each O
-         * block in Kb0s / Kb1s, l and m in Vb0s (each object holds 4 x 16 x 64 floats) */
-        static_assert(KS * KT * 64 * 2 >= QW * 16 * 64 * 4, "merge exchange fits a tile buffer");
-        float *X0 = reinterpret_cast<float *>(Kb0s) + wave * 16 * 64 + lane;
-        float *X1 = reinterpret_cast<float *>(Kb1s) + wave * 16 * 64 + lane;
-        float *X2 = reinterpret_cast<float *>(Vb0s) + wave * 2 * 64 + lane;
+         * block, waves 0-3 in Kb0s / Kb1s (each object holds 4 x 16 x 64 floats), waves 4-5 in
+         * Vb0s / Vb1s, and l and m in Vb0s after them */
+        static_assert(KS * KT * 64 * 2 >= 4 * 16 * 64 * 4 && QW <= 6, "merge exchange fits the tile buffers");
+        float *const xk0 = reinterpret_cast<float *>(Kb0s), *const xk1 = reinterpret_cast<float *>(Kb1s);
+        float *const xv0 = reinterpret_cast<float *>(Vb0s), *const xv1 = reinterpret_cast<float *>(Vb1s);
+        float *X0 = (wave < 4 ? xk0 + wave * 16 * 64 : xv0 + (wave - 4) * 16 * 64) + lane;
+        float *X1 = (wave < 4 ? xk1 + wave * 16 * 64 : xv1 + (wave - 4) * 16 * 64) + lane;
+        float *X2 = xv0 + (QW > 4 ? 2 * 16 * 64 : 0) + wave * 2 * 64 + lane;
         if (half == 1) {
 #pragma unroll
             for (int r = 0; r < 16; r++) { X0[r * 64] = oacc[0][r]; X1[r * 64] = oacc[1][r]; }
@@ -438,21 +441,32 @@ extern "C" hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, co
     a.scale_log2 = 0.125f * ARIA_LOG2E;
     /* split the keys inside the workgroup when there are enough tiles for both halves
      * (S = 1296 self-attention: 21 tiles); short key sets (the 256 cross keys) run one half.
-     * Query waves per half: 4 for the split form (two 8-wave workgroups per CU; 3 waves, 448
-     * blocks of 96 instead of 352 of 128 at S = 1296, measured 10 % slower), else the fewest
-     * query slots on the busiest CU (ceil(T / 256) blocks of 32 QW queries), ties to 4: the
-     * cross attention at S = 1296, 32 heads takes 3 (10.6 -> 10.4 us) */
+     * A CU running two workgroups takes nearly twice as long as one running a single one, so
+     * the split form takes the fewest query waves per half (4, 5 or 6) whose blocks give every
+     * CU at most one workgroup, else 4 (two per CU): S = 1296, 32 heads: 6, 224 blocks of 192
+     * queries (31.9 -> 27.8 us against 352 blocks of 128; the same bits). The one-half form
+     * takes the fewest query slots on the busiest CU (ceil(T / 256) blocks of 32 QW queries),
+     * ties to 4: the cross attention at S = 1296, 32 heads takes 3 (10.8 -> 10.4 us) */
     const bool split = (Nk + KT - 1) / KT >= 8;
     int qw = 4;
-    if (!split) {
+    if (split) {
+        for (int w = 4; w <= 6; w++)
+            if ((long)((Nq + 32 * w - 1) / (32 * w)) * BH <= 256) { qw = w; break; }
+    } else {
         const long t4 = (long)((Nq + 127) / 128) * BH, t3 = (long)((Nq + 95) / 96) * BH;
         if ((t3 + 255) / 256 * 3 < (t4 + 255) / 256 * 4) qw = 3;
     }
     a.nqb = (Nq + 32 * qw - 1) / (32 * qw);
     a.T = a.nqb * BH;
     const dim3 grid((a.T + 7) / 8 * 8);
-    if (split) hipLaunchKernelGGL((k_flash_attn<2, 4>), grid, dim3(512), 0, s, a);
-    else if (qw == 3) hipLaunchKernelGGL((k_flash_attn<1, 3>), grid, dim3(192), 0, s, a);
-    else hipLaunchKernelGGL((k_flash_attn<1, 4>), grid, dim3(256), 0, s, a);
+    if (split) {
+        if (qw == 6) hipLaunchKernelGGL((k_flash_attn<2, 6>), grid, dim3(768), 0, s, a);
+        else if (qw == 5) hipLaunchKernelGGL((k_flash_attn<2, 5>), grid, dim3(640), 0, s, a);
+        else hipLaunchKernelGGL((k_flash_attn<2, 4>), grid, dim3(512), 0, s, a);
+    } else if (qw == 3) {
+        hipLaunchKernelGGL((k_flash_attn<1, 3>), grid, dim3(192), 0, s, a);
+    } else {
+        hipLaunchKernelGGL((k_flash_attn<1, 4>), grid, dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }

@@ -21,11 +21,12 @@ def f16r(a):
 
 
 @pytest.mark.parametrize("B,H,Nq,Nk", [(1, 8, 48, 48), (2, 16, 1296, 1296), (2, 16, 1296, 256), (1, 2, 130, 77),
-                                       (2, 1, 1, 1), (1, 3, 200, 1300), (4, 16, 1024, 1024), (4, 16, 1024, 300)])
+                                       (2, 1, 1, 1), (1, 3, 200, 1300), (4, 16, 1024, 1024), (4, 16, 1024, 300),
+                                       (1, 24, 1296, 1296)])
 def test_flash_attention(hip, port, B, H, Nq, Nk):
-    """Every workgroup form: the keys split in two halves (Nk >= 512; 4 query waves) or not,
-    with 3 query waves (1296 queries x 32 heads, the small cases) or 4 (1024 x 64); ragged
-    query and key counts."""
+    """Every workgroup form: the keys split in two halves (Nk >= 512) with 4 query waves per
+    half (1024 x 64 heads, the small cases), 5 (1296 x 24) or 6 (1296 x 32), or one half with
+    3 query waves (1296 x 32, the small cases) or 4 (1024 x 64); ragged query and key counts."""
     r = rng(B * 1000 + Nq + Nk)
     q = f16r(randn(r, (B * H, Nq, 64))); k = f16r(randn(r, (B * H, Nk, 64))); v = f16r(randn(r, (B * H, Nk, 64)))
     out = np.empty((B, Nq, H * 64), np.float32)
