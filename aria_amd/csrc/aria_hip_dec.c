@@ -19,7 +19,7 @@
  *   nothing is copied back. Per block (src/aria_taae.c:93-162):
  *     h16    = dyt(seq, pre_norm)                      k_dec_dyt (block 0; later blocks get it
  *                                                      from the previous ff_out's epilogue)
- *     qkv    = h16 . to_qkv^T                          k_qgemm
+ *     qkv    = h16 . to_qkv^T, q/k DyT + RoPE          k_qgemm (DYT_ROPE epilogue)
  *     m16    = diff-attention per (chunk, head)        k_dec_attn
  *     seq   += m16 . to_out^T; h16 = dyt(seq, ff_norm) k_qgemm (ADD_DYT epilogue)
  *     g16    = silu(gate) * value of h16 . ff_in^T + b k_qgemm (GLU epilogue)
@@ -266,6 +266,27 @@ static int gemm_add_dyt(float *x, const uint16_t *m16, const uint16_t *w, const 
     return 0;
 }
 
+/* qkv = h16 . to_qkv^T with the q / k sections DynamicTanh-normed (qn, kn) and rotated at
+ * their chunk position (rcos / rsin [34, 16]) in the GEMM's epilogue, the order of
+ * src/aria_taae.c:120-127 */
+static int gemm_qkv(const aria_cuda_dec *h, const dec_blk *b, float *qkv, const uint16_t *h16, int M,
+                    hipStream_t s) {
+    aria_qgemm_epi e;
+    memset(&e, 0, sizeof e);
+    e.mode = ARIA_EPI_DYT_ROPE;
+    e.rows_per_batch = DS;
+    e.heads = DD / 64;
+    e.w[0] = b->qn_g; e.w[1] = b->qn_b; e.w[2] = b->kn_g; e.w[3] = b->kn_b;
+    e.eps = b->qn_alpha;
+    e.eps2 = b->kn_alpha;
+    e.cos_t = h->rcos;
+    e.sin_t = h->rsin;
+    e.rot = 2 * DRH;
+    STEP(aria_k_qgemm_e(qkv, 0, h16, 1, ARIA_WF16, b->to_qkv, NULL, NULL, M, DD, DQKV, 0, 0, &e, s),
+         "k_qgemm (decoder to_qkv + q/k DyT + RoPE)");
+    return 0;
+}
+
 /* one block on the nch chunks of 34 rows at x, in place (src/aria_taae.c:93-162). h16 (rows
  * aligned with x) holds dyt(x, pre_norm) on entry; the to_out GEMM's epilogue writes
  * dyt(x, ff_norm) into it, and ff_out's writes the next block's pre_norm DyT when `next` is given
@@ -274,9 +295,8 @@ static int block(const aria_cuda_dec *h, const dec_blk *b, const dec_blk *next, 
                  uint16_t *h16, int nch, hipStream_t s) {
     const int N = nch * DS;
     int rc;
-    if ((rc = gemm(w->qkv, 0, h16, b->to_qkv, NULL, N, DD, DQKV, ARIA_EPI_STORE, s))) return rc;
-    STEP(aria_k_dec_attn(w->m16, w->qkv, b->qn_alpha, b->qn_g, b->qn_b, b->kn_alpha, b->kn_g, b->kn_b, h->rcos,
-                         h->rsin, nch, s), "k_dec_attn");
+    if ((rc = gemm_qkv(h, b, w->qkv, h16, N, s))) return rc;
+    STEP(aria_k_dec_attn(w->m16, w->qkv, nch, s), "k_dec_attn");
     if ((rc = gemm_add_dyt(x, w->m16, b->to_out, NULL, N, DD, h16, b->ff_alpha, b->ff_g, b->ff_b, s))) return rc;
     if ((rc = gemm(w->g16, 1, h16, b->ff_in, b->ff_in_b, N, DD, 2 * DINNER, ARIA_EPI_GLU, s))) return rc;
     if (next) return gemm_add_dyt(x, w->g16, b->ff_out, b->ff_out_b, N, DINNER, h16, next->pre_alpha, next->pre_g,

@@ -114,19 +114,24 @@ enum { ARIA_WQ8 = 0, ARIA_WQ4 = 1, ARIA_WF16 = 2, ARIA_WI8 = 3 };
  *   GLU       columns interleave (value, gate) pairs: y[m][c/2] = silu(gate) * value,
  *             [M, N/2], fp16 or fp32 (y_f16) (the weight rows were interleaved when packed)
  *   ADD_DYT   ADD, then also dst[0][m][c] = half(tanh(eps * y) * w[0][c] + w[1][c]) of the new y
- *             (the next DynamicTanh norm's GEMM operand; eps carries alpha; fp16 weights only) */
+ *             (the next DynamicTanh norm's GEMM operand; eps carries alpha; fp16 weights only)
+ *   DYT_ROPE  the decoder's attention operands: N = 5 sections of heads*64 columns (q | k | v |
+ *             qd | kd); per head dim d, q and qd become tanh(eps x) * w[0][d] + w[1][d], k and
+ *             kd tanh(eps2 x) * w[2][d] + w[3][d], then rotate-half RoPE over the first rot
+ *             dims (8, 16 or 32) at position m % rows_per_batch (cos_t / sin_t
+ *             [rows_per_batch, rot / 2]); v as it is; y fp32 [M, N] (fp16 weights only) */
 enum { ARIA_EPI_STORE = 0, ARIA_EPI_GATE_RES = 1, ARIA_EPI_ADD = 2, ARIA_EPI_HEADS = 3, ARIA_EPI_GLU = 4,
-       ARIA_EPI_ADD_DYT = 5 };
+       ARIA_EPI_ADD_DYT = 5, ARIA_EPI_DYT_ROPE = 6 };
 typedef struct {
     int mode, rows_per_batch;
     const float *gate, *add2, *gate2;
     int gate_bs, gate2_bs;
     int heads, nsec, kind[3];
     uint16_t *dst[3];
-    const float *w[3];
+    const float *w[4];
     const float *cos_t, *sin_t;
     int rot;
-    float eps;
+    float eps, eps2;
 } aria_qgemm_epi;
 hipError_t aria_k_qgemm(void *y, int y_f16, const void *x, int x_f16, int wtype, const void *q,
                         const float *scale, const float *bias, int M, int K, int N, hipStream_t s);
@@ -186,17 +191,15 @@ hipError_t aria_k_conv1d(float *out, const float *in, const float *w, const floa
  *   dec_expand: seq [Tp * 17, 768]: group t = x[t] (zeros for t >= T), then 16 new_tokens
  *   dec_dyt:    y fp16 = tanh(alpha x) * g + b over [rows, 768]
  *   dec_attn:   merged fp16 [nch * 34, 768] = the differential attention of each chunk from
- *               qkv [nch * 34, 3840] (q | k | v | qd | kd), q/k DynamicTanh norms and RoPE
- *               (rcos/rsin [34, 16]) applied inside
+ *               qkv [nch * 34, 3840] (q | k | v | qd | kd), whose q/k sections already carry
+ *               the DynamicTanh norms and RoPE (the to_qkv GEMM's DYT_ROPE epilogue)
  *   dec_im2col: xc fp32 [Lt, 2304] = the k3 mapping convolution's input rows
  *   dec_map:    audio [2, M * 256] = unpatch(xc [M, 2304] . W [512, 2304]^T + b), fp32 MFMA */
 hipError_t aria_k_dec_in(uint16_t *xt, const float *lat, int T, float std, hipStream_t s);
 hipError_t aria_k_dec_expand(float *seq, const float *x, const float *tok, int T, int Tp, hipStream_t s);
 hipError_t aria_k_dec_dyt(uint16_t *y, const float *x, float alpha, const float *g, const float *b, int rows,
                           hipStream_t s);
-hipError_t aria_k_dec_attn(uint16_t *merged, const float *qkv, float qa, const float *qg, const float *qb,
-                           float ka, const float *kg, const float *kb, const float *rcos, const float *rsin,
-                           int nch, hipStream_t s);
+hipError_t aria_k_dec_attn(uint16_t *merged, const float *qkv, int nch, hipStream_t s);
 hipError_t aria_k_dec_im2col(float *xc, const float *seq, int Lt, int Lout, hipStream_t s);
 hipError_t aria_k_dec_map(float *audio, const float *xc, const float *W, const float *b, int M, hipStream_t s);
 

@@ -8,16 +8,16 @@
  *   k_dec_in      softnorm inverse and transpose: latent [256, T] * std -> fp16 [T, 256]
  *   k_dec_expand  the 17-token groups: frame t's projected token, then 16 new_tokens
  *   k_dec_dyt     DynamicTanh norm tanh(alpha x) * gamma + beta -> fp16 GEMM operand
- *   k_dec_attn_mfma  one chunk-head of the differential self-attention, fused: the q/k
- *                 DynamicTanh norms, RoPE (32 rotated dims), both softmax(q k^T / 8) v
- *                 products over the chunk's 34 tokens on the fp32 MFMA, their difference,
- *                 merged fp16
+ *   k_dec_attn_mfma  one chunk-head of the differential self-attention, fused: both
+ *                 softmax(q k^T / 8) v products over the chunk's 34 tokens on the fp32 MFMA,
+ *                 their difference, merged fp16 (the q/k DynamicTanh norms and RoPE, 32
+ *                 rotated dims, are the to_qkv GEMM's DYT_ROPE epilogue)
  *   k_dec_im2col  the k = 3 mapping convolution's input rows (the last 16 of each group)
  *   k_dec_map     the mapping convolution as an fp32 GEMM on the fp32 MFMA (the reference
  *                 keeps it fp32), trimmed to T * 16 rows and unpatched to stereo in its stores
  * Arithmetic follows the reference's order (built with -ffp-contract=off); the DyT norms use
- * the device library's tanhf, the attention's q/k norms tanh_fast (exp + rcp, a few 1e-7
- * absolute) and the softmax exponential v_exp_f32 (~1 ulp).
+ * the device library's tanhf, the q/k norms tanh_fast (exp + rcp, a few 1e-7 absolute) and the
+ * softmax exponential v_exp_f32 (~1 ulp).
  */
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
@@ -74,21 +74,19 @@ __global__ __launch_bounds__(256) void k_dec_dyt(uint2 *y, const float4 *x, floa
 
 struct DecAttnArgs {
     uint16_t *merged;           /* [nch * 34, 768] fp16 */
-    const float *qkv;           /* [nch * 34, 3840]: q | k | v | qd | kd */
-    const float *qg, *qb, *kg, *kb;
-    float qa, ka;
-    const float *rcos, *rsin;   /* [34, 16] */
+    const float *qkv;           /* [nch * 34, 3840]: q | k | v | qd | kd, q / k normed and rotated */
 };
 
 /* ---- the chunk attention on the fp32 MFMA (v_mfma_f32_16x16x4_f32) ----
  * One (chunk, head) per workgroup of two waves; wave w computes pair w (0: q, k; 1: qd, kd)
- * over the chunk's 34 tokens padded to 48 (3 blocks of 16):
+ * over the chunk's 34 tokens padded to 48 (3 blocks of 16). The q / k sections of qkv arrive
+ * DynamicTanh-normed and rotated (the to_qkv GEMM's DYT_ROPE epilogue, once per element):
+ * done here, that prologue was the kernel's bound.
  *   v (34 rows x 64 dims, shared by both pairs) travels to LDS by LDS DMA first thing, so
- *     its fetch overlaps the q / k work and takes no registers
+ *     its fetch overlaps the q / k loads and takes no registers
  *   S = q k^T: 3 x 3 blocks, 16 k-steps; lane l supplies row l % 16 of q (A) and of k (B) at
  *     dim 16 (l / 16) + s in step s, so each lane loads 16 consecutive dims of one row from
- *     qkv, applies the DynamicTanh norm and RoPE in registers (the rotation's partner dim
- *     d +- 16 sits in lane l ^ 16, same row) and keeps them as its operands
+ *     qkv and keeps them as its operands
  *   softmax over the 34 valid keys in the accumulators (a row's 16 columns of a block sit in
  *     16 lanes: xor-shuffle reductions), probabilities through LDS into the A layout
  *   O = P v: 3 x 4 blocks, 12 k-steps over keys 12 (l / 16) + s; output block j column n
@@ -126,23 +124,11 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
         }
     }
 
-    /* this lane's 16 dims (16 lq ..) of q (or qd) and k (or kd) rows 16 b + lr, normalised
-     * and rotated */
+    /* this lane's 16 dims (16 lq ..) of q (or qd) and k (or kd) rows 16 b + lr; rows past the
+     * chunk are zero */
     float qf[3][16], kf[3][16];
     {
         const int qo = wave ? 2304 : 0, ko = wave ? 3072 : 768;
-        float qg[16], qb[16], kg[16], kb[16];
-#pragma unroll
-        for (int j4 = 0; j4 < 4; j4++) {
-            const float4 g0 = reinterpret_cast<const float4 *>(a.qg + lq * 16)[j4];
-            const float4 b0 = reinterpret_cast<const float4 *>(a.qb + lq * 16)[j4];
-            const float4 g1 = reinterpret_cast<const float4 *>(a.kg + lq * 16)[j4];
-            const float4 b1 = reinterpret_cast<const float4 *>(a.kb + lq * 16)[j4];
-            qg[4 * j4] = g0.x; qg[4 * j4 + 1] = g0.y; qg[4 * j4 + 2] = g0.z; qg[4 * j4 + 3] = g0.w;
-            qb[4 * j4] = b0.x; qb[4 * j4 + 1] = b0.y; qb[4 * j4 + 2] = b0.z; qb[4 * j4 + 3] = b0.w;
-            kg[4 * j4] = g1.x; kg[4 * j4 + 1] = g1.y; kg[4 * j4 + 2] = g1.z; kg[4 * j4 + 3] = g1.w;
-            kb[4 * j4] = b1.x; kb[4 * j4 + 1] = b1.y; kb[4 * j4 + 2] = b1.z; kb[4 * j4 + 3] = b1.w;
-        }
 #pragma unroll
         for (int b = 0; b < 3; b++) {
             const int r = b * 16 + lr;
@@ -152,39 +138,10 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
             for (int j4 = 0; j4 < 4; j4++) {
                 const float4 x = *reinterpret_cast<const float4 *>(row + qo + 4 * j4);
                 const float4 y = *reinterpret_cast<const float4 *>(row + ko + 4 * j4);
-                qf[b][4 * j4 + 0] = x.x; qf[b][4 * j4 + 1] = x.y; qf[b][4 * j4 + 2] = x.z; qf[b][4 * j4 + 3] = x.w;
-                kf[b][4 * j4 + 0] = y.x; kf[b][4 * j4 + 1] = y.y; kf[b][4 * j4 + 2] = y.z; kf[b][4 * j4 + 3] = y.w;
-            }
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                qf[b][j] = ok ? tanh_fast(a.qa * qf[b][j]) * qg[j] + qb[j] : 0.0f;
-                kf[b][j] = ok ? tanh_fast(a.ka * kf[b][j]) * kg[j] + kb[j] : 0.0f;
-            }
-            /* RoPE on dims 0..31: lanes lq = 0 hold d < 16, lq = 1 hold d + 16 */
-            const int rc = ok ? r : 0;
-            float cs[16], sn[16];
-#pragma unroll
-            for (int j4 = 0; j4 < 4; j4++) {
-                const float4 c4 = reinterpret_cast<const float4 *>(a.rcos + rc * DEC_RH)[j4];
-                const float4 s4 = reinterpret_cast<const float4 *>(a.rsin + rc * DEC_RH)[j4];
-                cs[4 * j4] = c4.x; cs[4 * j4 + 1] = c4.y; cs[4 * j4 + 2] = c4.z; cs[4 * j4 + 3] = c4.w;
-                sn[4 * j4] = s4.x; sn[4 * j4 + 1] = s4.y; sn[4 * j4 + 2] = s4.z; sn[4 * j4 + 3] = s4.w;
-            }
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float pq = __shfl_xor(qf[b][j], 16), pk = __shfl_xor(kf[b][j], 16);
-                if (lq < 2) {
-                    const float c = cs[j], sv = sn[j];
-                    if (lq == 0) {
-                        const float q0 = qf[b][j] * c, q1 = pq * sv, k0 = kf[b][j] * c, k1 = pk * sv;
-                        qf[b][j] = ok ? q0 - q1 : 0.0f;
-                        kf[b][j] = ok ? k0 - k1 : 0.0f;
-                    } else {
-                        const float q0 = qf[b][j] * c, q1 = pq * sv, k0 = kf[b][j] * c, k1 = pk * sv;
-                        qf[b][j] = ok ? q0 + q1 : 0.0f;
-                        kf[b][j] = ok ? k0 + k1 : 0.0f;
-                    }
-                }
+                qf[b][4 * j4 + 0] = ok ? x.x : 0.0f; qf[b][4 * j4 + 1] = ok ? x.y : 0.0f;
+                qf[b][4 * j4 + 2] = ok ? x.z : 0.0f; qf[b][4 * j4 + 3] = ok ? x.w : 0.0f;
+                kf[b][4 * j4 + 0] = ok ? y.x : 0.0f; kf[b][4 * j4 + 1] = ok ? y.y : 0.0f;
+                kf[b][4 * j4 + 2] = ok ? y.z : 0.0f; kf[b][4 * j4 + 3] = ok ? y.w : 0.0f;
             }
         }
     }
@@ -444,13 +401,10 @@ extern "C" hipError_t aria_k_dec_dyt(uint16_t *y, const float *x, float alpha, c
                        (const float4 *)g, (const float4 *)b, n4);
     return hipGetLastError();
 }
-extern "C" hipError_t aria_k_dec_attn(uint16_t *merged, const float *qkv, float qa, const float *qg, const float *qb,
-                                      float ka, const float *kg, const float *kb, const float *rcos, const float *rsin,
-                                      int nch, hipStream_t s) {
+extern "C" hipError_t aria_k_dec_attn(uint16_t *merged, const float *qkv, int nch, hipStream_t s) {
     if (nch <= 0) return hipSuccess;
     DecAttnArgs a;
-    a.merged = merged; a.qkv = qkv; a.qg = qg; a.qb = qb; a.kg = kg; a.kb = kb; a.qa = qa; a.ka = ka;
-    a.rcos = rcos; a.rsin = rsin;
+    a.merged = merged; a.qkv = qkv;
     hipLaunchKernelGGL(k_dec_attn_mfma, dim3(nch * 12), dim3(128), 0, s, a, 12);
     return hipGetLastError();
 }

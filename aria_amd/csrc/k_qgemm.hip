@@ -474,7 +474,15 @@ extern "C" hipError_t aria_k_qgemm_e(void *y, int y_f16, const void *x, int x_f1
             !a.epi.w[0] || !a.epi.w[1] || ((uintptr_t)a.epi.dst[0] & 7u) || ((uintptr_t)a.epi.w[0] & 15u) ||
             ((uintptr_t)a.epi.w[1] & 15u))
             return hipErrorInvalidValue;
-    } else if (a.epi.mode > ARIA_EPI_ADD_DYT || a.epi.mode < 0) {
+    } else if (a.epi.mode == ARIA_EPI_DYT_ROPE) {   /* the decoder's to_qkv only */
+        const aria_qgemm_epi &e = a.epi;
+        const int rot = e.rot;
+        bool ok = wtype == ARIA_WF16 && x_f16 && !y_f16 && !a.gelu && e.heads > 0 && N == 5 * 64 * e.heads &&
+                  e.rows_per_batch > 0 && (rot == 0 || rot == 8 || rot == 16 || rot == 32);
+        for (int i = 0; ok && i < 4; i++) ok = e.w[i] && ((uintptr_t)e.w[i] & 15u) == 0;
+        if (ok && rot) ok = e.cos_t && e.sin_t && ((uintptr_t)e.cos_t & 15u) == 0 && ((uintptr_t)e.sin_t & 15u) == 0;
+        if (!ok) return hipErrorInvalidValue;
+    } else if (a.epi.mode > ARIA_EPI_DYT_ROPE || a.epi.mode < 0) {
         return hipErrorInvalidValue;
     } else if (a.epi.mode != ARIA_EPI_STORE) {
         if (y_f16 || a.epi.rows_per_batch <= 0) return hipErrorInvalidValue;

@@ -458,6 +458,9 @@ static void launch_big(const QArgs &a, hipStream_t s) {
             if constexpr (FN >= 2) launch_big_m<WT, FM, FN, ARIA_EPI_HEADS, false, MINB, KSPL>(a, s);
             break;
         case ARIA_EPI_GLU: launch_big_m<WT, FM, FN, ARIA_EPI_GLU, false, MINB, KSPL>(a, s); break;
+        case ARIA_EPI_DYT_ROPE:
+            if constexpr (WT == ARIA_WF16) launch_big_m<WT, FM, FN, ARIA_EPI_DYT_ROPE, false, MINB, KSPL>(a, s);
+            break;
         default:
             if (a.gelu) launch_big_m<WT, FM, FN, ARIA_EPI_STORE, true, MINB, KSPL>(a, s);
             else launch_big_m<WT, FM, FN, ARIA_EPI_STORE, false, MINB, KSPL>(a, s);

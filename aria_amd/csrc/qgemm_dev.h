@@ -107,6 +107,7 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
                 }
                 return;
             case ARIA_EPI_GLU: epilogue<FM, FN, WT, ARIA_EPI_GLU>(a, acc, E, lane, mw, nw); return;   /* no GELU */
+            case ARIA_EPI_DYT_ROPE: epilogue<FM, FN, WT, ARIA_EPI_DYT_ROPE>(a, acc, E, lane, mw, nw); return;   /* no GELU */
             default:
                 if (g) epilogue<FM, FN, WT, ARIA_EPI_STORE, true>(a, acc, E, lane, mw, nw);
                 else epilogue<FM, FN, WT, ARIA_EPI_STORE>(a, acc, E, lane, mw, nw);
@@ -173,11 +174,30 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
         first = d0 < rh;
         i0 = first ? d0 : d0 - rh;
     }
-    /* HEADS: (batch, position) of this lane's current row, m = hb * S + hs. The rows a lane
-     * visits rise by RPI per store (and per 32-row group, NIT * RPI = 32), so the pair is
-     * advanced by (RPI / S, RPI % S) with one carry instead of a division per row. */
+    /* DYT_ROPE: the lane's section kind (0 q-like, 1 k-like, 2 v), DynamicTanh gain (gw),
+     * bias (dbv) and alpha, and its RoPE lanes. A wave's 32 FN columns start on a multiple of
+     * 32, so the rotation partner d +- rot / 2 (rot <= 32) of the lane's four dims sits rot / 8
+     * lanes away in the same row: lane ^ (rot / 8). */
+    float4 dbv = make_float4(0.f, 0.f, 0.f, 0.f);
+    float dal = 0.0f;
+    if constexpr (MODE == ARIA_EPI_DYT_ROPE) {
+        const int sec = nb / (e.heads * 64), d0 = nb & 63;
+        kind = (!col_ok || sec == 2) ? 2 : (sec == 0 || sec == 3) ? 0 : 1;
+        if (kind != 2) {
+            gw = *reinterpret_cast<const float4 *>((kind == 0 ? e.w[0] : e.w[2]) + d0);
+            dbv = *reinterpret_cast<const float4 *>((kind == 0 ? e.w[1] : e.w[3]) + d0);
+            dal = kind == 0 ? e.eps : e.eps2;
+        }
+        rh = e.rot >> 1;
+        rope = kind != 2 && e.rot > 0 && d0 < e.rot;
+        first = d0 < rh;
+        i0 = first ? d0 : d0 - rh;
+    }
+    /* HEADS, DYT_ROPE: (batch, position) of this lane's current row, m = hb * S + hs. The rows
+     * a lane visits rise by RPI per store (and per 32-row group, NIT * RPI = 32), so the pair
+     * is advanced by (RPI / S, RPI % S) with one carry instead of a division per row. */
     int hb = 0, hs = 0, hq = 0, hr = 0;
-    if constexpr (MODE == ARIA_EPI_HEADS) {
+    if constexpr (MODE == ARIA_EPI_HEADS || MODE == ARIA_EPI_DYT_ROPE) {
         const int S = e.rows_per_batch, m0 = mw + erow;
         hb = m0 / S;
         hs = m0 - hb * S;
@@ -282,6 +302,47 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
                     const float h2 = tanh_fast(al * o.z) * dg.z + db.z, h3 = tanh_fast(al * o.w) * dg.w + db.w;
                     *reinterpret_cast<uint2 *>(e.dst[0] + (size_t)m * a.N + nb) = make_uint2(pack2h(h0, h1), pack2h(h2, h3));
                 }
+            }
+        } else if constexpr (MODE == ARIA_EPI_DYT_ROPE) {
+            /* tanh(alpha x) * g + b, then the rotation with the partner's normed value, in the
+             * order of the reference's per-head norms and rotation (src/aria_taae.c:120-127) */
+            const int S = e.rows_per_batch;
+            float4 cs[NIT], sn[NIT];
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                if (rope) {   /* hs < S: the table row is in range past M too */
+                    cs[it] = *reinterpret_cast<const float4 *>(e.cos_t + (size_t)hs * rh + i0);
+                    sn[it] = *reinterpret_cast<const float4 *>(e.sin_t + (size_t)hs * rh + i0);
+                }
+                hs += hr;
+                hb += hq;
+                if (hs >= S) { hs -= S; hb++; }
+            }
+            const float gv[4] = {gw.x, gw.y, gw.z, gw.w}, dv[4] = {dbv.x, dbv.y, dbv.z, dbv.w};
+#pragma unroll
+            for (int it = 0; it < NIT; it++) {
+                float *w4 = v[it];
+                if (kind != 2) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) w4[q] = tanh_fast(dal * w4[q]) * gv[q] + dv[q];
+                }
+                if (e.rot > 0) {   /* uniform: every lane takes part in the exchange */
+                    float p[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) p[q] = __shfl_xor(w4[q], rh >> 2);
+                    if (rope) {
+                        const float cv[4] = {cs[it].x, cs[it].y, cs[it].z, cs[it].w};
+                        const float sv[4] = {sn[it].x, sn[it].y, sn[it].z, sn[it].w};
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const float c0 = w4[q] * cv[q], s1 = p[q] * sv[q];
+                            w4[q] = first ? c0 - s1 : c0 + s1;
+                        }
+                    }
+                }
+                const int m = mrow[it];
+                if (m < a.M && col_ok)
+                    *reinterpret_cast<float4 *>((float *)a.y + (size_t)m * a.N + nb) = make_float4(w4[0], w4[1], w4[2], w4[3]);
             }
         } else {   /* HEADS */
             const int S = e.rows_per_batch;
