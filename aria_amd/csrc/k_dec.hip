@@ -78,129 +78,140 @@ struct DecAttnArgs {
 };
 
 /* ---- the chunk attention on the fp32 MFMA (v_mfma_f32_16x16x4_f32) ----
- * One (chunk, head) per workgroup of two waves; wave w computes pair w (0: q, k; 1: qd, kd)
- * over the chunk's 34 tokens padded to 48 (3 blocks of 16). The q / k sections of qkv arrive
- * DynamicTanh-normed and rotated (the to_qkv GEMM's DYT_ROPE epilogue, once per element):
- * done here, that prologue was the kernel's bound.
- *   v (34 rows x 64 dims, shared by both pairs) travels to LDS by LDS DMA first thing, so
+ * One (chunk, head) per workgroup of six waves; wave w computes pair p = w / 3 (0: q, k;
+ * 1: qd, kd) for the 16 queries of block i = w % 3 of the chunk's 34 tokens padded to 48
+ * (3 blocks of 16). The q / k sections of qkv arrive DynamicTanh-normed and rotated (the
+ * to_qkv GEMM's DYT_ROPE epilogue, once per element). Against one wave per pair (288 MFMAs in
+ * one wave's chain, 129 VGPRs, three waves per SIMD) each wave runs 96 MFMAs at 58 VGPRs:
+ * decode 0.698 -> 0.686 ms at T = 108, 2.71 -> 2.63 ms at T = 646, same bits.
+ *   v (34 rows x 64 dims, shared by all six waves) travels to LDS by LDS DMA first thing, so
  *     its fetch overlaps the q / k loads and takes no registers
- *   S = q k^T: 3 x 3 blocks, 16 k-steps; lane l supplies row l % 16 of q (A) and of k (B) at
- *     dim 16 (l / 16) + s in step s, so each lane loads 16 consecutive dims of one row from
- *     qkv and keeps them as its operands
+ *   each wave loads its block's 16 q rows and 16 k rows once; the k rows go through LDS to the
+ *     pair's other two waves (loading all 48 per wave doubled the L2 reads: slower at T = 2584)
+ *   S = q k^T for the wave's query block: 1 x 3 blocks, 16 k-steps; lane l supplies row l % 16
+ *     of q (A) and of k (B) at dim 16 (l / 16) + s in step s (16 consecutive dims of one row)
  *   softmax over the 34 valid keys in the accumulators (a row's 16 columns of a block sit in
- *     16 lanes: xor-shuffle reductions), probabilities through LDS into the A layout
- *   O = P v: 3 x 4 blocks, 12 k-steps over keys 12 (l / 16) + s; output block j column n
+ *     16 lanes: xor-shuffle reductions), probabilities through the wave's own 16 LDS rows
+ *     (over the k space, once every wave's k reads are done) into the A layout
+ *   O = P v: 1 x 4 blocks, 12 k-steps over keys 12 (l / 16) + s; output block j column n
  *     holds dim 4 n + j, so a lane's B operands of a step are one 16-byte LDS read of v and
  *     its four output dims of a row are adjacent (one 8-byte store)
- * Wave 1 leaves O in LDS (lane-major, over the v / P space once both products are done),
- * wave 0 writes half(O0 - O1) to the merged rows. Accumulator v of lane l in a 16 x 16
- * block: row 4 (l / 16) + v, column l % 16. Padded q / k rows are zero and padded keys are
- * masked before the max and multiply zero v, so nothing past the chunk's rows is used. fp32
- * operands, as the reference keeps this attention fp32. */
+ * The pair-1 waves leave O in LDS (lane-major, over the v space once every product is done),
+ * the pair-0 wave of the same block writes half(O0 - O1) to the merged rows. Accumulator v of
+ * lane l in a 16 x 16 block: row 4 (l / 16) + v, column l % 16. Padded q / k rows are zero and
+ * padded keys are masked before the max and multiply zero v, so nothing past the chunk's rows
+ * is used. Every output element is the same sequence of operations as with one wave per pair.
+ * fp32 operands, as the reference keeps this attention fp32. */
 #define DA_P 48            /* padded chunk */
 #define DA_PS 52           /* LDS row stride of P (floats; 16-byte aligned rows) */
+#define DA_KS 68           /* LDS row stride of k (floats; rows spread over the banks) */
 #define DA_VCH 576         /* v staging: 16-byte chunks (34 rows x 16, rounded up to 9 x 64) */
+#define DA_WAVES 6
 
 typedef float f32x4_dec __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
-    /* [0, 9216): v rows (256 B each); [9216, 9216 + 2 * 48 * 52 * 4): P of the two waves;
-     * after both products: O of wave 1 (48 x 64 floats, lane-major) from offset 0 */
-    __shared__ __attribute__((aligned(16))) float sm[DA_VCH * 4 + 2 * DA_P * DA_PS];
+/* this lane's 16 dims (16 lq ..) of row r of the section at column off; rows past the chunk
+ * are zero */
+__device__ __forceinline__ void dec_ld_row(float (&f)[16], const float *base, int off, int r, int lq) {
+    const bool ok = r < DEC_S;
+    const float *row = base + (size_t)(ok ? r : 0) * DEC_QKV + off + lq * 16;
+#pragma unroll
+    for (int j4 = 0; j4 < 4; j4++) {
+        const float4 x = *reinterpret_cast<const float4 *>(row + 4 * j4);
+        f[4 * j4 + 0] = ok ? x.x : 0.0f; f[4 * j4 + 1] = ok ? x.y : 0.0f;
+        f[4 * j4 + 2] = ok ? x.z : 0.0f; f[4 * j4 + 3] = ok ? x.w : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(64 * DA_WAVES) void k_dec_attn_mfma(DecAttnArgs a, int H) {
+    /* [0, 9216): v rows (256 B each); then k of both pairs (2 x 48 rows x 68 floats), later
+     * reused for P (6 waves x 16 rows x 52); after every product: O of the pair-1 waves (3 x
+     * 16 x 64 floats, lane-major) from offset 0 */
+    __shared__ __attribute__((aligned(16))) float sm[DA_VCH * 4 + 2 * 48 * DA_KS];
+    static_assert(2 * 48 * DA_KS >= DA_WAVES * 16 * DA_PS, "P fits the k space");
     float4 *Vs = reinterpret_cast<float4 *>(sm);
     const int ch = blockIdx.x / H, h = blockIdx.x % H;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int pair = wave / 3, qi = wave % 3;
     const int lr = lane & 15, lq = lane >> 4;
     const float *base = a.qkv + (size_t)ch * DEC_S * DEC_QKV + h * DEC_HD;
 
     /* v by LDS DMA: instruction i moves chunks 64 i .. 64 i + 63 (row p / 16, dims 4 (p % 16)
-     * ..), wave w the instructions i = w, w + 2, ..; chunks past the 34 rows re-read row 33 */
+     * ..), wave w the instructions i = w, w + 6; chunks past the 34 rows re-read row 33 */
     {
         typedef __attribute__((address_space(3))) void lds_void_t;
-        for (int i = wave; i < DA_VCH / 64; i += 2) {
+        for (int i = wave; i < DA_VCH / 64; i += DA_WAVES) {
             const int p = 64 * i + lane, r = min(p >> 4, DEC_S - 1);
             __builtin_amdgcn_global_load_lds(base + (size_t)r * DEC_QKV + 1536 + 4 * (p & 15),
                                              (lds_void_t *)(sm + 256 * i), 16, 0, 0);
         }
     }
-
-    /* this lane's 16 dims (16 lq ..) of q (or qd) and k (or kd) rows 16 b + lr; rows past the
-     * chunk are zero */
-    float qf[3][16], kf[3][16];
+    /* q (or qd) rows 16 qi + lr in registers; k (or kd) rows 16 qi + lr through LDS to the
+     * pair's three waves */
+    float qf[16], kf[3][16];
+    float *Ks = sm + DA_VCH * 4 + pair * (48 * DA_KS);
     {
-        const int qo = wave ? 2304 : 0, ko = wave ? 3072 : 768;
+        float kr[16];
+        dec_ld_row(qf, base, pair ? 2304 : 0, qi * 16 + lr, lq);
+        dec_ld_row(kr, base, pair ? 3072 : 768, qi * 16 + lr, lq);
 #pragma unroll
-        for (int b = 0; b < 3; b++) {
-            const int r = b * 16 + lr;
-            const bool ok = r < DEC_S;
-            const float *row = base + (size_t)(ok ? r : 0) * DEC_QKV + lq * 16;
-#pragma unroll
-            for (int j4 = 0; j4 < 4; j4++) {
-                const float4 x = *reinterpret_cast<const float4 *>(row + qo + 4 * j4);
-                const float4 y = *reinterpret_cast<const float4 *>(row + ko + 4 * j4);
-                qf[b][4 * j4 + 0] = ok ? x.x : 0.0f; qf[b][4 * j4 + 1] = ok ? x.y : 0.0f;
-                qf[b][4 * j4 + 2] = ok ? x.z : 0.0f; qf[b][4 * j4 + 3] = ok ? x.w : 0.0f;
-                kf[b][4 * j4 + 0] = ok ? y.x : 0.0f; kf[b][4 * j4 + 1] = ok ? y.y : 0.0f;
-                kf[b][4 * j4 + 2] = ok ? y.z : 0.0f; kf[b][4 * j4 + 3] = ok ? y.w : 0.0f;
-            }
-        }
+        for (int j4 = 0; j4 < 4; j4++)
+            *reinterpret_cast<float4 *>(Ks + (qi * 16 + lr) * DA_KS + lq * 16 + 4 * j4) =
+                make_float4(kr[4 * j4], kr[4 * j4 + 1], kr[4 * j4 + 2], kr[4 * j4 + 3]);
     }
-
-    /* S = q k^T */
-    f32x4_dec sc[3][3];
+    __syncthreads();   /* the pair's 48 k rows in LDS */
 #pragma unroll
-    for (int i = 0; i < 3; i++)
+    for (int bk = 0; bk < 3; bk++)
 #pragma unroll
-        for (int j = 0; j < 3; j++) sc[i][j] = f32x4_dec{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j4 = 0; j4 < 4; j4++) {
+            const float4 k4 = *reinterpret_cast<const float4 *>(Ks + (bk * 16 + lr) * DA_KS + lq * 16 + 4 * j4);
+            kf[bk][4 * j4] = k4.x; kf[bk][4 * j4 + 1] = k4.y; kf[bk][4 * j4 + 2] = k4.z; kf[bk][4 * j4 + 3] = k4.w;
+        }
+    /* S = q k^T for the wave's query block */
+    f32x4_dec sc[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) sc[j] = f32x4_dec{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int st = 0; st < 16; st++)
 #pragma unroll
-        for (int i = 0; i < 3; i++)
-#pragma unroll
-            for (int j = 0; j < 3; j++)
-                sc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[i][st], kf[j][st], sc[i][j], 0, 0, 0);
+        for (int j = 0; j < 3; j++) sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[st], kf[j][st], sc[j], 0, 0, 0);
+    __syncthreads();   /* every wave's k reads done before P overwrites them */
 
     /* softmax of each row over keys < 34 (block 2 holds keys 32 + lr) */
-    float *P = sm + DA_VCH * 4 + wave * (DA_P * DA_PS);
+    float *P = sm + DA_VCH * 4 + wave * (16 * DA_PS);
 #pragma unroll
-    for (int i = 0; i < 3; i++)
+    for (int v = 0; v < 4; v++) {
+        float x0 = sc[0][v] * 0.125f, x1 = sc[1][v] * 0.125f;
+        float x2 = lr < DEC_S - 32 ? sc[2][v] * 0.125f : -INFINITY;
+        float mx = fmaxf(fmaxf(x0, x1), x2);
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            float x0 = sc[i][0][v] * 0.125f, x1 = sc[i][1][v] * 0.125f;
-            float x2 = lr < DEC_S - 32 ? sc[i][2][v] * 0.125f : -INFINITY;
-            float mx = fmaxf(fmaxf(x0, x1), x2);
+        for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        x0 = exp_fast(x0 - mx); x1 = exp_fast(x1 - mx); x2 = exp_fast(x2 - mx);
+        float sum = (x0 + x1) + x2;
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-            x0 = exp_fast(x0 - mx); x1 = exp_fast(x1 - mx); x2 = exp_fast(x2 - mx);
-            float sum = (x0 + x1) + x2;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o);
-            const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-            const int row = i * 16 + 4 * lq + v;
-            P[row * DA_PS + lr] = x0 * inv;
-            P[row * DA_PS + 16 + lr] = x1 * inv;
-            P[row * DA_PS + 32 + lr] = x2 * inv;
-        }
-
-    /* v in LDS: this wave's transfers done (vmcnt), then the barrier publishes both waves' */
+        for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o);
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        const int row = 4 * lq + v;
+        P[row * DA_PS + lr] = x0 * inv;
+        P[row * DA_PS + 16 + lr] = x1 * inv;
+        P[row * DA_PS + 32 + lr] = x2 * inv;
+    }
+    /* v in LDS: this wave's transfers done (vmcnt), then the barrier publishes every wave's
+     * (and orders each wave's P stores before its reads below) */
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
 
     /* O = P v over keys 12 lq + s (keys >= 34 have P = 0 and multiply zero v) */
-    f32x4_dec oc[3][4];
+    f32x4_dec oc[4];
 #pragma unroll
-    for (int i = 0; i < 3; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) oc[i][j] = f32x4_dec{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < 4; j++) oc[j] = f32x4_dec{0.0f, 0.0f, 0.0f, 0.0f};
     {
-        float pf[3][12];
+        float pf[12];
 #pragma unroll
-        for (int i = 0; i < 3; i++)
-#pragma unroll
-            for (int c4 = 0; c4 < 3; c4++) {
-                const float4 p4 = *reinterpret_cast<const float4 *>(&P[(i * 16 + lr) * DA_PS + lq * 12 + 4 * c4]);
-                pf[i][4 * c4 + 0] = p4.x; pf[i][4 * c4 + 1] = p4.y; pf[i][4 * c4 + 2] = p4.z; pf[i][4 * c4 + 3] = p4.w;
-            }
+        for (int c4 = 0; c4 < 3; c4++) {
+            const float4 p4 = *reinterpret_cast<const float4 *>(&P[lr * DA_PS + lq * 12 + 4 * c4]);
+            pf[4 * c4 + 0] = p4.x; pf[4 * c4 + 1] = p4.y; pf[4 * c4 + 2] = p4.z; pf[4 * c4 + 3] = p4.w;
+        }
 #pragma unroll
         for (int s2 = 0; s2 < 12; s2++) {
             const int key = lq * 12 + s2;
@@ -208,39 +219,31 @@ __global__ __launch_bounds__(128) void k_dec_attn_mfma(DecAttnArgs a, int H) {
             const bool kv = key < DEC_S;
             const float vf[4] = {kv ? v4.x : 0.0f, kv ? v4.y : 0.0f, kv ? v4.z : 0.0f, kv ? v4.w : 0.0f};
 #pragma unroll
-            for (int i = 0; i < 3; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    oc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pf[i][s2], vf[j], oc[i][j], 0, 0, 0);
+            for (int j = 0; j < 4; j++) oc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(pf[s2], vf[j], oc[j], 0, 0, 0);
         }
     }
-
-    /* both products done before wave 1's O overwrites v and P */
+    /* every product done before the pair-1 waves' O overwrites v and P */
     __syncthreads();
-    float *Os = sm;
-    if (wave == 1) {
+    float *Os = sm + qi * (16 * 64);
+    if (pair == 1) {
 #pragma unroll
-        for (int i = 0; i < 3; i++)
+        for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) Os[((i * 4 + j) * 4 + v) * 64 + lane] = oc[i][j][v];
+            for (int v = 0; v < 4; v++) Os[(j * 4 + v) * 64 + lane] = oc[j][v];
     }
     __syncthreads();
-    if (wave == 0) {
+    if (pair == 0) {
         uint2 *dst = reinterpret_cast<uint2 *>(a.merged + (size_t)ch * DEC_S * DEC_D + h * DEC_HD + 4 * lr);
 #pragma unroll
-        for (int i = 0; i < 3; i++)
+        for (int v = 0; v < 4; v++) {
+            const int row = qi * 16 + 4 * lq + v;
+            if (row < DEC_S) {
+                uint32_t hv[4];
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int row = i * 16 + 4 * lq + v;
-                if (row < DEC_S) {
-                    uint32_t hv[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) hv[j] = f2h_bits(oc[i][j][v] - Os[((i * 4 + j) * 4 + v) * 64 + lane]);
-                    dst[(size_t)row * (DEC_D / 4)] = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
-                }
+                for (int j = 0; j < 4; j++) hv[j] = f2h_bits(oc[j][v] - Os[(j * 4 + v) * 64 + lane]);
+                dst[(size_t)row * (DEC_D / 4)] = make_uint2(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16));
             }
+        }
     }
 }
 
@@ -405,7 +408,7 @@ extern "C" hipError_t aria_k_dec_attn(uint16_t *merged, const float *qkv, int nc
     if (nch <= 0) return hipSuccess;
     DecAttnArgs a;
     a.merged = merged; a.qkv = qkv;
-    hipLaunchKernelGGL(k_dec_attn_mfma, dim3(nch * 12), dim3(128), 0, s, a, 12);
+    hipLaunchKernelGGL(k_dec_attn_mfma, dim3(nch * 12), dim3(64 * DA_WAVES), 0, s, a, 12);
     return hipGetLastError();
 }
 extern "C" hipError_t aria_k_dec_im2col(float *xc, const float *seq, int Lt, int Lout, hipStream_t s) {
