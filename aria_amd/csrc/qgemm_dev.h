@@ -204,8 +204,29 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
         hq = RPI / S;
         hr = RPI - hq * S;
     }
+    /* GATE_RES, ADD, ADD_DYT: the fp32 residual rows (and the per-row gates or second addend)
+     * of 32-row group i + 1 are requested as group i starts, so a group's load latency runs
+     * under the previous group's staging and stores instead of after them (two groups of
+     * registers, buffer i & 1) */
+    constexpr bool RMW = MODE == ARIA_EPI_GATE_RES || MODE == ARIA_EPI_ADD || MODE == ARIA_EPI_ADD_DYT;
+    float4 rr_b[2][NIT], g2_b[2][NIT];
+    auto rmw_load = [&](int i, float4 (&rr)[NIT], float4 (&g2)[NIT]) __attribute__((always_inline)) {
+        const int nbc = col_ok ? nb : 0;
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int mc = min(mw + i * 32 + it * RPI + erow, a.M - 1);
+            rr[it] = *reinterpret_cast<const float4 *>((const float *)a.y + (size_t)mc * a.N + nbc);
+            if (MODE == ARIA_EPI_GATE_RES && !gpre) g2[it] = gate_at(mc / e.rows_per_batch, nbc);
+            else if (MODE == ARIA_EPI_ADD && e.add2)
+                g2[it] = *reinterpret_cast<const float4 *>(e.add2 + (size_t)mc * a.N + nbc);
+        }
+    };
+    if constexpr (RMW) rmw_load(0, rr_b[0], g2_b[0]);
 #pragma unroll
     for (int i = 0; i < FM; i++) {
+        if constexpr (RMW) {
+            if (i + 1 < FM) rmw_load(i + 1, rr_b[(i + 1) & 1], g2_b[(i + 1) & 1]);
+        }
 #pragma unroll
         for (int j = 0; j < FN; j++)
 #pragma unroll
@@ -260,23 +281,13 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
                     *reinterpret_cast<float2 *>((float *)a.y + (size_t)m * (a.N >> 1) + (nb >> 1)) = make_float2(g0, g1);
             }
         } else if constexpr (MODE == ARIA_EPI_GATE_RES || MODE == ARIA_EPI_ADD || MODE == ARIA_EPI_ADD_DYT) {
-            /* read-modify-write of the fp32 residual: all loads first, then all stores */
-            float4 rr[NIT], g2[NIT];
+            /* read-modify-write of the fp32 residual (loaded one group ahead) */
             float4 dg = make_float4(0.f, 0.f, 0.f, 0.f), db = dg;   /* ADD_DYT: the norm's gain and bias */
             if constexpr (MODE == ARIA_EPI_ADD_DYT) {
                 if (col_ok) {
                     dg = *reinterpret_cast<const float4 *>(e.w[0] + nb);
                     db = *reinterpret_cast<const float4 *>(e.w[1] + nb);
                 }
-            }
-            const int nbc = col_ok ? nb : 0;
-#pragma unroll
-            for (int it = 0; it < NIT; it++) {
-                const int mc = min(mrow[it], a.M - 1);
-                rr[it] = *reinterpret_cast<const float4 *>((const float *)a.y + (size_t)mc * a.N + nbc);
-                if (MODE == ARIA_EPI_GATE_RES && !gpre) g2[it] = gate_at(mc / e.rows_per_batch, nbc);
-                else if (MODE == ARIA_EPI_ADD && e.add2)
-                    g2[it] = *reinterpret_cast<const float4 *>(e.add2 + (size_t)mc * a.N + nbc);
             }
 #pragma unroll
             for (int it = 0; it < NIT; it++) {
@@ -287,13 +298,13 @@ __device__ __forceinline__ void epilogue(const QArgs &a, AccT (&acc)[FM][FN], fl
                     /* y += v * sigmoid(1 - gate): the rounding order of k_gate_residual */
                     float4 sg;
                     if (gpre) sg = (m < bnd) ? gs0 : gs1;
-                    else sg = make_float4(gate_sig_f(g2[it].x), gate_sig_f(g2[it].y), gate_sig_f(g2[it].z), gate_sig_f(g2[it].w));
-                    o = make_float4(rr[it].x + v[it][0] * sg.x, rr[it].y + v[it][1] * sg.y,
-                                    rr[it].z + v[it][2] * sg.z, rr[it].w + v[it][3] * sg.w);
+                    else sg = make_float4(gate_sig_f(g2_b[i & 1][it].x), gate_sig_f(g2_b[i & 1][it].y), gate_sig_f(g2_b[i & 1][it].z), gate_sig_f(g2_b[i & 1][it].w));
+                    o = make_float4(rr_b[i & 1][it].x + v[it][0] * sg.x, rr_b[i & 1][it].y + v[it][1] * sg.y,
+                                    rr_b[i & 1][it].z + v[it][2] * sg.z, rr_b[i & 1][it].w + v[it][3] * sg.w);
                 } else {
-                    o = make_float4(rr[it].x + v[it][0], rr[it].y + v[it][1], rr[it].z + v[it][2], rr[it].w + v[it][3]);
+                    o = make_float4(rr_b[i & 1][it].x + v[it][0], rr_b[i & 1][it].y + v[it][1], rr_b[i & 1][it].z + v[it][2], rr_b[i & 1][it].w + v[it][3]);
                     if (MODE == ARIA_EPI_ADD && e.add2)
-                        o = make_float4(o.x + g2[it].x, o.y + g2[it].y, o.z + g2[it].z, o.w + g2[it].w);
+                        o = make_float4(o.x + g2_b[i & 1][it].x, o.y + g2_b[i & 1][it].y, o.z + g2_b[i & 1][it].z, o.w + g2_b[i & 1][it].w);
                 }
                 *reinterpret_cast<float4 *>((float *)a.y + (size_t)m * a.N + nb) = o;
                 if constexpr (MODE == ARIA_EPI_ADD_DYT) {
