@@ -82,11 +82,11 @@ __device__ __forceinline__ float norm_elem_c(float xv, float inv, float mu, floa
     return n;
 }
 
+/* t1 = 1 + scale, formed once per column with the broadcast vectors (the same fp32 add) */
 template <int EPI>
-__device__ __forceinline__ float epi_elem(float n, float xv, float sc, float sh) {
+__device__ __forceinline__ float epi_elem(float n, float xv, float t1, float sh) {
     if (EPI & EPI_MOD) {
-        float t = 1.0f + sc;
-        n = n * t;
+        n = n * t1;
         n = n + sh;
     }
     if (EPI & EPI_GELU) n = gelu_tanh_f(n);
@@ -141,6 +141,7 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
                 sc = make_float4(sc.x + sa.x, sc.y + sa.y, sc.z + sa.z, sc.w + sa.w);
                 sh = make_float4(sh.x + ha.x, sh.y + ha.y, sh.z + ha.z, sh.w + ha.w);
             }
+            sc = make_float4(1.0f + sc.x, 1.0f + sc.y, 1.0f + sc.z, 1.0f + sc.w);   /* the 1 + scale factor */
         }
     };
     bool shared_done = false;
