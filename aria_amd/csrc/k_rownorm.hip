@@ -98,7 +98,7 @@ __device__ __forceinline__ float epi_elem(float n, float xv, float t1, float sh)
  * With a full wave per row (LPR = 64) and any broadcast vector (gain, bias, scale, shift),
  * the workgroup's four rows share them (RMSNorm with its gain alone: 5.30 -> 5.14 us at
  * [2592, 1024]): the 256 lanes load each vector once into LDS
- * (forming scale + scale_add and shift + shift_add there, once), and every wave reads its lanes'
+ * (forming 1 + (scale + scale_add) and shift + shift_add there, once), and every wave reads its lanes'
  * parts back from LDS. Per row that replaces 4-20 KB of L1 requests by one LDS read of the same
  * bytes (a CU reads 3x more per clock from LDS than from L1). A workgroup whose rows straddle
  * two batches of the modulation loads per lane as before. */
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
     const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 wv[VPL], bv[VPL], scv[VPL], shv[VPL];
-    /* the vectors of batch bt at float4 column c4 */
+    /* the vectors of batch bt at float4 column c4; sc returns the modulation factor 1 + scale */
     auto vecs_at = [&](int bt, int c4, float4 &w, float4 &b, float4 &sc, float4 &sh) __attribute__((always_inline)) {
         w = (EPI & EPI_W) ? w4[c4] : z4;
         b = (EPI & EPI_B) ? b4[c4] : z4;
