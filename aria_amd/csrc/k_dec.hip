@@ -266,7 +266,9 @@ __global__ __launch_bounds__(256) void k_dec_im2col(float *xc, const float *seq,
  * v_mfma_f32_32x32x2_f32 keeps fp32 operands, as the reference keeps this GEMM in fp32.
  * 256 threads = 2 x 2 waves, each owning FM x FN blocks of 32 x 32 (tile 64 FM rows of xc by
  * 64 FN rows of W); k moves through LDS 32 at a time, double-buffered (one barrier per
- * slice), the next slice's global loads in flight during the current slice's MFMAs. The
+ * slice), the next slice's global loads in flight during the current slice's MFMAs. KS = 2
+ * doubles the workgroup: the second 256 threads take the second half of k on their own
+ * buffers and hand their partial sums to the first (acc_first + acc_second). The
  * MFMA computes W xc^T, so a lane's accumulators hold 4 consecutive n of one m: 4
  * consecutive audio samples, one 16-byte store. Lane l of an MFMA supplies row l % 32 at
  * k = 16 (l / 32) + j of the slice, j = 0..15 (any fixed k order gives the dot product),
@@ -279,15 +281,20 @@ __global__ __launch_bounds__(256) void k_dec_im2col(float *xc, const float *seq,
 
 typedef float f32x16_dec __attribute__((ext_vector_type(16)));
 
-template <int FM, int FN>
-__global__ __launch_bounds__(256) void k_dec_map(float *audio, const float *xc, const float *W, const float *bias, int M) {
+template <int FM, int FN, int KS>
+__global__ __launch_bounds__(256 * KS) void k_dec_map(float *audio, const float *xc, const float *W, const float *bias, int M) {
     constexpr int BM = 64 * FM, BN = 64 * FN;
     constexpr int LA = BM * MAP_KT / 4 / 256, LW = BN * MAP_KT / 4 / 256;   /* float4 loads per thread */
-    __shared__ __attribute__((aligned(16))) float As[2][BM * MAP_SA];
-    __shared__ __attribute__((aligned(16))) float Ws[2][BN * MAP_SA];
+    /* KS = 2: threads 256.. (waves 4-7) run the second half of k on their own buffers, and
+     * their partial sums join the first half's through LDS before the stores */
+    __shared__ __attribute__((aligned(16))) float As_all[KS][2][BM * MAP_SA];
+    __shared__ __attribute__((aligned(16))) float Ws_all[KS][2][BN * MAP_SA];
+    static_assert(MAP_K % (MAP_KT * KS) == 0, "the k halves are whole slices");
+    const int khalf = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+
     const int ntile = MAP_N / BN;
     const int m0 = (blockIdx.x / ntile) * BM, n0 = (blockIdx.x % ntile) * BN;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x & 255, wave = tid >> 6, lane = tid & 63;
     const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
 
     f32x16_dec acc[FM][FN];
@@ -304,10 +311,10 @@ __global__ __launch_bounds__(256) void k_dec_map(float *audio, const float *xc, 
             float4 xa[FM], wa[FN];
 #pragma unroll
             for (int i = 0; i < FM; i++)
-                xa[i] = *reinterpret_cast<const float4 *>(&As[buf][(wm * 32 * FM + i * 32 + lr) * MAP_SA + lh * 16 + q4 * 4]);
+                xa[i] = *reinterpret_cast<const float4 *>(&As_all[khalf][buf][(wm * 32 * FM + i * 32 + lr) * MAP_SA + lh * 16 + q4 * 4]);
 #pragma unroll
             for (int j = 0; j < FN; j++)
-                wa[j] = *reinterpret_cast<const float4 *>(&Ws[buf][(wn * 32 * FN + j * 32 + lr) * MAP_SA + lh * 16 + q4 * 4]);
+                wa[j] = *reinterpret_cast<const float4 *>(&Ws_all[khalf][buf][(wn * 32 * FN + j * 32 + lr) * MAP_SA + lh * 16 + q4 * 4]);
 #pragma unroll
             for (int e = 0; e < 4; e++)
 #pragma unroll
@@ -320,15 +327,17 @@ __global__ __launch_bounds__(256) void k_dec_map(float *audio, const float *xc, 
 
     /* per thread: float4 q = tid + 256 i of the slice, row q / 8, column 4 (q % 8) */
     const float *ga[LA], *gw[LW];
+    constexpr int NK = MAP_K / MAP_KT / KS;   /* slices of this half */
+    const int k0 = khalf * NK * MAP_KT;
 #pragma unroll
     for (int i = 0; i < LA; i++) {
         const int q = tid + i * 256;
-        ga[i] = xc + (size_t)min(m0 + (q >> 3), M - 1) * MAP_K + (q & 7) * 4;
+        ga[i] = xc + (size_t)min(m0 + (q >> 3), M - 1) * MAP_K + k0 + (q & 7) * 4;
     }
 #pragma unroll
     for (int i = 0; i < LW; i++) {
         const int q = tid + i * 256;
-        gw[i] = W + (size_t)(n0 + (q >> 3)) * MAP_K + (q & 7) * 4;
+        gw[i] = W + (size_t)(n0 + (q >> 3)) * MAP_K + k0 + (q & 7) * 4;
     }
     const int so = (tid >> 3) * MAP_SA + (tid & 7) * 4;   /* + 32 rows per i */
     float4 ra[LA], rw[LW];
@@ -337,11 +346,10 @@ __global__ __launch_bounds__(256) void k_dec_map(float *audio, const float *xc, 
 #pragma unroll
     for (int i = 0; i < LW; i++) rw[i] = *reinterpret_cast<const float4 *>(gw[i]);
 #pragma unroll
-    for (int i = 0; i < LA; i++) *reinterpret_cast<float4 *>(&As[0][so + i * 32 * MAP_SA]) = ra[i];
+    for (int i = 0; i < LA; i++) *reinterpret_cast<float4 *>(&As_all[khalf][0][so + i * 32 * MAP_SA]) = ra[i];
 #pragma unroll
-    for (int i = 0; i < LW; i++) *reinterpret_cast<float4 *>(&Ws[0][so + i * 32 * MAP_SA]) = rw[i];
+    for (int i = 0; i < LW; i++) *reinterpret_cast<float4 *>(&Ws_all[khalf][0][so + i * 32 * MAP_SA]) = rw[i];
     __syncthreads();
-    constexpr int NK = MAP_K / MAP_KT;
     for (int kt = 0; kt < NK; kt++) {
         const int cur = kt & 1;
         if (kt + 1 < NK) {
@@ -353,12 +361,38 @@ __global__ __launch_bounds__(256) void k_dec_map(float *audio, const float *xc, 
         compute(cur);
         if (kt + 1 < NK) {
 #pragma unroll
-            for (int i = 0; i < LA; i++) *reinterpret_cast<float4 *>(&As[cur ^ 1][so + i * 32 * MAP_SA]) = ra[i];
+            for (int i = 0; i < LA; i++) *reinterpret_cast<float4 *>(&As_all[khalf][cur ^ 1][so + i * 32 * MAP_SA]) = ra[i];
 #pragma unroll
-            for (int i = 0; i < LW; i++) *reinterpret_cast<float4 *>(&Ws[cur ^ 1][so + i * 32 * MAP_SA]) = rw[i];
+            for (int i = 0; i < LW; i++) *reinterpret_cast<float4 *>(&Ws_all[khalf][cur ^ 1][so + i * 32 * MAP_SA]) = rw[i];
         }
         __syncthreads();
     }
+
+    if constexpr (KS == 2) {
+        /* every wave is past its last LDS read (the loop's closing barrier): the second half's
+         * partial sums go through its own buffers, lane-major, and the first half adds them
+         * (acc_first + acc_second, a fixed order) and stores */
+        float *X = &As_all[1][0][0] + tid;
+        static_assert(FM * FN * 16 * 256 <= 2 * BM * MAP_SA, "the partial sums fit the second half's buffers");
+        if (khalf == 1) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) X[((i * FN + j) * 16 + r) * 256] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (khalf == 0) {
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = acc[i][j][r] + X[((i * FN + j) * 16 + r) * 256];
+        }
+    }
+    if (KS == 2 && khalf == 1) return;
 
     /* accumulator r of lane l: n = 8 (r / 4) + 4 (l / 32) + r % 4, m = l % 32 (per block) */
 #pragma unroll
@@ -421,6 +455,13 @@ extern "C" hipError_t aria_k_dec_im2col(float *xc, const float *seq, int Lt, int
 extern "C" hipError_t aria_k_dec_map(float *audio, const float *xc, const float *W, const float *b, int M,
                                      hipStream_t s) {
     if (M <= 0) return hipSuccess;
-    hipLaunchKernelGGL((k_dec_map<1, 1>), dim3((M + 63) / 64 * (MAP_N / 64)), dim3(256), 0, s, audio, xc, W, b, M);
+    /* at most one tile per CU (T <= 128: 216 tiles at T = 108): the k range split over two
+     * 4-wave halves gives each SIMD two waves (decode 0.688 -> 0.658 ms at T = 108); more tiles
+     * keep one 4-wave workgroup per tile (the split measured 0.5 % slower at T = 646) */
+    const int tiles = (M + 63) / 64 * (MAP_N / 64);
+    if (tiles <= 256)
+        hipLaunchKernelGGL((k_dec_map<1, 1, 2>), dim3(tiles), dim3(512), 0, s, audio, xc, W, b, M);
+    else
+        hipLaunchKernelGGL((k_dec_map<1, 1, 1>), dim3(tiles), dim3(256), 0, s, audio, xc, W, b, M);
     return hipGetLastError();
 }
