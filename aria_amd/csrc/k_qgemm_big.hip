@@ -487,7 +487,7 @@ static void launch_big(const QArgs &a, hipStream_t s) {
 #define BIG_CFGS(X) X(0, 3, 1, 2, 1) X(1, 4, 1, 2, 1) X(2, 2, 2, 2, 1) X(3, 6, 1, 2, 1) X(4, 7, 1, 2, 1) X(5, 3, 1, 1, 2)
 static const int big_fm[] = {3, 4, 2, 6, 7, 3};
 static const int big_fn[] = {1, 1, 2, 1, 1, 1};
-static const int big_ks[] = {1, 1, 1, 1, 1, 2};   /* 2: the K range split inside the workgroup */   /* 2: the K range split inside the workgroup */
+static const int big_ks[] = {1, 1, 1, 1, 1, 2};   /* 2: the K range split inside the workgroup */
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
 
