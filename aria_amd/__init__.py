@@ -76,7 +76,6 @@ SIGNATURES = {
     "aria_hip_add_dev": (_i, [_P, _P, _P, _sz, _P]),
     "aria_hip_axpy_dev": (_i, [_P, _P, _f, _sz, _P]),
     "aria_hip_scale_dev": (_i, [_P, _P, _f, _sz, _P]),
-    "aria_hip_micro_dev": (_i, [_i, _i, _i, _P, _P, _P]),
     "aria_hip_gelu_tanh_dev": (_i, [_P, _P, _sz, _P]),
     "aria_hip_silu_dev": (_i, [_P, _P, _sz, _P]),
     "aria_hip_silu_gate_dev": (_i, [_P, _P, _P, _sz, _P]),

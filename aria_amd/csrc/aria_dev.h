@@ -129,8 +129,10 @@ __device__ __forceinline__ float gelu_tanh_f(float v) {
 /* tanh through tanh(x) = 1 - 2/(e^{2x} + 1): v_exp_f32, an add, v_rcp_f32 and an fma, where
  * the device library's tanhf takes ~30 instructions with branches. Absolute error a few
  * 1e-7 (near 0 the subtraction cancels, so the relative error grows as 1e-7/|x| while the
- * absolute error stays); the limits are exact: e^{2x} -> inf gives 1, -> 0 gives -1. For the
- * DynamicTanh norms feeding attention scores, whose gate (1e-3 + 5e-3 * max) is far wider. */
+ * absolute error stays); the limits are exact: e^{2x} -> inf gives 1, -> 0 gives -1. Used by
+ * the decoder's DynamicTanh norms inside GEMM epilogues (the q/k norms of DYT_ROPE and the
+ * block norms of ADD_DYT, whose outputs are rounded to fp16 right after), where the error
+ * is far inside the decoder's gate (1e-3 + 5e-3 * max). */
 __device__ __forceinline__ float tanh_fast(float x) {
     return __builtin_fmaf(-2.0f, rcp_fast(__builtin_amdgcn_exp2f(x * (2.0f * ARIA_LOG2E)) + 1.0f), 1.0f);
 }

@@ -352,12 +352,6 @@ int aria_hip_scale_dev(float *dy, const float *dx, float a, size_t n, void *stre
     KCK(aria_k_scale(dy, dx, a, n, pick(stream)), "k_scale");
     return 0;
 }
-int aria_hip_micro_dev(int which, int grid, int iters, float *dout, const void *dtab, void *stream) {
-    ENSURE();
-    REQ(which >= 0 && which <= 5 && grid > 0 && iters > 0 && dout && (which != 5 || dtab));
-    KCK(aria_k_micro(which, grid, iters, dout, dtab, pick(stream)), "k_micro");
-    return 0;
-}
 int aria_hip_gelu_tanh_dev(float *dy, const float *dx, size_t n, void *stream) {
     ENSURE();
     REQ(n == 0 || (dy && dx));

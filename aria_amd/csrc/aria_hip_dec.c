@@ -342,6 +342,7 @@ static int ws_ensure(aria_cuda_dec *h, int T, dec_ws *w) {
         f_free(h->ws);
         h->ws = NULL;
         h->ws_T = 0;
+        h->ws_bytes = 0;
         int rc = d_alloc(&h->ws, need);
         if (rc) return rc;
         h->ws_bytes = need;

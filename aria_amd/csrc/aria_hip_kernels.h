@@ -48,8 +48,6 @@ hipError_t aria_k_rownorm_ada_q8(int8_t *yq, float *sx, const float *x, const fl
 hipError_t aria_k_add(float *y, const float *a, const float *b, size_t n, hipStream_t s);
 hipError_t aria_k_scale(float *y, const float *x, float a, size_t n, hipStream_t s);
 hipError_t aria_k_axpy(float *y, const float *x, float a, size_t n, hipStream_t s);
-/* measurement probes (k_micro.hip) */
-hipError_t aria_k_micro(int which, int grid, int iters, float *out, const void *tab, hipStream_t s);
 hipError_t aria_k_gelu_tanh(float *y, const float *x, size_t n, hipStream_t s);
 hipError_t aria_k_silu(float *y, const float *x, size_t n, hipStream_t s);
 hipError_t aria_k_softcap(float *y, const float *x, float cap, size_t n, hipStream_t s);

@@ -15,9 +15,11 @@
  *   k_dec_im2col  the k = 3 mapping convolution's input rows (the last 16 of each group)
  *   k_dec_map     the mapping convolution as an fp32 GEMM on the fp32 MFMA (the reference
  *                 keeps it fp32), trimmed to T * 16 rows and unpatched to stereo in its stores
- * Arithmetic follows the reference's order (built with -ffp-contract=off); the DyT norms use
- * the device library's tanhf, the q/k norms tanh_fast (exp + rcp, a few 1e-7 absolute) and the
- * softmax exponential v_exp_f32 (~1 ulp).
+ * Arithmetic follows the reference's order (built with -ffp-contract=off). tanh: block 0's pre
+ * norm (k_dec_dyt) uses the device library's tanhf; the other 11 block norms (the ADD_DYT
+ * epilogue of to_out / ff_out) and the q/k norms (the DYT_ROPE epilogue of to_qkv) use
+ * tanh_fast (exp + rcp, a few 1e-7 absolute, before the fp16 rounding of the GEMM operand);
+ * the softmax exponential is v_exp_f32 (~1 ulp).
  */
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"

@@ -545,6 +545,8 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
         else launch_big<ARIA_WQ4, fm, fn, mb, ks>(a, s);                 \
         break;
     if (wt != ARIA_WQ8 && wt != ARIA_WQ4) return hipErrorInvalidValue;
+    /* the Q4 [min, step] pairs of a K-tile move 16 bytes at a time */
+    if (wt == ARIA_WQ4 && ((uintptr_t)a.scale & 15u)) return hipErrorInvalidValue;
     switch (cfg) {
         BIG_CFGS(BIG_CASE)
         default: return hipErrorInvalidValue;

@@ -1,8 +1,9 @@
 /*
- * k_micro.hip - issue-rate and bandwidth probes of the MI355X (gfx950) that the kernel designs
+ * probe_micro.hip - issue-rate and bandwidth probes of the MI355X (gfx950) that the kernel designs
  * lean on: the fp16 MFMA rate, the issue cost of a wave64 fp32 FMA, exp2 and reciprocal, and the
- * LDS and L1 read bandwidth per CU. Measurement only (bench.py --micro); no op of the library
- * uses them.
+ * LDS and L1 read bandwidth per CU. Measurement only: built into its own library,
+ * aria_amd/libaria_probe.so, which bench.py --micro loads; the product library does not contain
+ * these kernels.
  *
  * Every probe runs a fixed number of iterations of independent dependency chains per wave, so
  * the unit under test, not latency, sets the pace, and folds its chains into one store per lane
@@ -15,8 +16,8 @@
  *   MICRO_L1    8 global_load_dwordx4 per lane and iteration from a 16 KB table per workgroup
  *               (resident in the CU's L1 after the first pass)                -> bytes / s
  */
-#include "aria_dev.h"
-#include "aria_hip_kernels.h"
+#include <hip/hip_runtime.h>
+#include <stdint.h>
 
 typedef float f32x16_m __attribute__((ext_vector_type(16)));
 typedef _Float16 half8_m __attribute__((ext_vector_type(8)));
@@ -108,9 +109,12 @@ __global__ __launch_bounds__(256) void k_micro_l1(float *out, const uint4 *tab, 
     out[(size_t)blockIdx.x * 256 + t] = (float)s;
 }
 
-/* which: MICRO_* above (0..5); out: grid * 256 floats; tab (MICRO_L1 only): grid * 16 KB */
-extern "C" hipError_t aria_k_micro(int which, int grid, int iters, float *out, const void *tab, hipStream_t s) {
+/* One launch of probe `which` (MICRO_* above, 0..5) with `grid` workgroups of 256 lanes and
+ * `iters` loop trips on `stream`; out: grid * 256 floats; tab (MICRO_L1 only): grid * 16 KB of
+ * device memory. Returns the hipError_t code of the launch (0 on success). */
+extern "C" int aria_probe_micro(int which, int grid, int iters, float *out, const void *tab, void *stream) {
     if (grid <= 0 || iters <= 0 || !out) return hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
     switch (which) {
         case 0: hipLaunchKernelGGL(k_micro_mfma, dim3(grid), dim3(256), 0, s, out, iters); break;
         case 1: hipLaunchKernelGGL(k_micro_valu<0>, dim3(grid), dim3(256), 0, s, out, iters, 0.999f, 0.001f); break;
@@ -123,5 +127,5 @@ extern "C" hipError_t aria_k_micro(int which, int grid, int iters, float *out, c
             break;
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
+    return (int)hipGetLastError();
 }

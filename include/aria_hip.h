@@ -241,14 +241,6 @@ int aria_hip_glu_combine(float *out, const float *proj, const float *bias, int r
 int aria_hip_add(float *y, const float *a, const float *b, size_t n);
 int aria_hip_pingpong(float *x, const float *v, const float *noise, float tc, float tn, size_t n);
 
-/* ---- measurement probes (no counterpart in the reference; bench.py --micro) ----
- * One launch of probe `which` (0 fp16 MFMA 32x32x16, 1 fp32 FMA, 2 exp2, 3 reciprocal, 4 LDS
- * reads, 5 L1-resident global reads) with `grid` workgroups of 256 lanes and `iters` loop trips,
- * on `stream`; dout: grid * 256 floats (the folded results); dtab (probe 5 only): grid * 16 KB
- * of device memory to read. Work per launch: probe 0 grid * 4 * iters * 4 MFMAs; probes 1-3
- * grid * 4 * iters * 8 wave instructions; probes 4-5 grid * 4 * iters * 8 KB. */
-int aria_hip_micro_dev(int which, int grid, int iters, float *dout, const void *dtab, void *stream);
-
 #ifdef __cplusplus
 }
 #endif
