@@ -136,7 +136,8 @@ struct Stage {
 
 /* One tile per workgroup; MINB workgroups per CU (MINB = 2 when the tile's registers and
  * LDS allow two: the second workgroup's waves cover one workgroup's barrier waits and its
- * epilogue). The tiles of an XCD are a contiguous run in M-major order (xcd_tile). */
+ * epilogue). The tiles of an XCD are a contiguous run in M-major order (xcd_tile). Wave w
+ * owns weight rows [32 FN w, 32 FN (w + 1)) and every activation row of the tile. */
 template <int WT, int FM, int FN, int MODE, bool GELU, int MINB, int NS, int NST, int KSPL>
 __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN, int T) {
     using St = Stage<WT, FM, FN>;   /* one 64-deep sub-tile; a pipeline stage holds NS of them */
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
     constexpr int EPI_WAVE = 32 * EPI_STRIDE;                          /* bytes per wave */
     static_assert(NST * SB >= 4 * EPI_WAVE, "the epilogue staging fits the stages");
     static_assert(KSPL == 1 || KSPL == 2, "one or two K halves");
-    static_assert(KSPL * NST * SB <= (MINB == 1 ? 160 : 80) * 1024, "the stages fit the LDS");
+    static_assert(KSPL * NST * SB <= 160 * 1024 / MINB, "the stages fit the LDS share of MINB workgroups");
     static_assert(KSPL == 1 || KSPL * NST * SB >= FM * FN * 16 * 256 * 4, "the second half's partial sums fit the stages");
     __shared__ __attribute__((aligned(16))) uint8_t smem_all[KSPL * NST * SB];
 
@@ -236,104 +237,103 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
     using AccT = typename std::conditional<WT == ARIA_WI8, i32x16_t, f32x16_t>::type;
     AccT acc[FM][FN];
 
-    /* one K-tile from stage B: this lane's raw weights from LDS, then 4 MFMA steps of FM x FN
-     * MFMAs; step ks + 1's activation fragments are requested and its weights unpacked while
-     * step ks's MFMAs run */
+    /* one K-tile from stage B in 4 MFMA steps of FM x FN MFMAs. The operands of step ks + 1
+     * (activation fragments from LDS; weight fragments from LDS, or unpacked in registers from
+     * this lane's raw Q8 / Q4 words read at the start of the K-tile) are requested while step
+     * ks's MFMAs run, and the order is pinned: each step is a scheduling region of its own in
+     * which every MFMA is followed by one LDS read and a share of the unpack VALU. Left to
+     * itself the scheduler sinks each fragment read next to its MFMA, and every MFMA then
+     * waits out an LDS latency. */
+    using FragT = typename std::conditional<WT == ARIA_WI8, i32x4_t, half8_t>::type;
+    constexpr int NMF = FM * FN;                                             /* MFMAs per step */
+    constexpr int NDS = FM + ((WT == ARIA_WF16 || WT == ARIA_WI8) ? FN : 0); /* LDS reads per step */
+    constexpr int NVU = (WT == ARIA_WQ4) ? 14 * FN : (WT == ARIA_WQ8) ? 10 * FN : 0;   /* unpack VALU */
+    auto pin = []() __attribute__((always_inline)) {
+        static_for<NMF>([&](auto I) __attribute__((always_inline)) {
+            constexpr int i = decltype(I)::value;
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       /* one MFMA */
+            constexpr int d = (NDS * (i + 1)) / NMF - (NDS * i) / NMF;
+            if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);  /* LDS reads */
+            constexpr int v = (NVU * (i + 1)) / NMF - (NVU * i) / NMF;
+            if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);  /* VALU */
+        });
+        __builtin_amdgcn_sched_barrier(0);
+    };
     auto compute = [&](auto BB) __attribute__((always_inline)) {
         constexpr int B = decltype(BB)::value;
         static_for<NS>([&](auto UU) __attribute__((always_inline)) {
         const uint8_t *S = smem + B * SB + decltype(UU)::value * St::BYTES;
-        if constexpr (WT == ARIA_WI8) {
-            /* W8A8: both operands straight from LDS, no unpack; lane half h covers k in
-             * [64 h, 64 h + 64) of the 128-k tile and step ks its 16 k at 64 h + 16 ks on both
-             * sides (the int32 sums are exact, so any common order gives the same bits) */
-            const uint16_t *X = reinterpret_cast<const uint16_t *>(S);
-            const uint16_t *Wr = reinterpret_cast<const uint16_t *>(S + St::A);
-            static_for<4>([&](auto KS) __attribute__((always_inline)) {
-                constexpr int ks = decltype(KS)::value;
-                i32x4_t xf[FM], wf[FN];
-#pragma unroll
-                for (int i = 0; i < FM; i++) xf[i] = *reinterpret_cast<const i32x4_t *>(&X[xo(i * 32 + lrow, 4 * lh + ks)]);
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-                    wf[j] = *reinterpret_cast<const i32x4_t *>(&Wr[xo(rbase + 32 * j + lrow, 4 * lh + ks)]);
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[j], xf[i], acc[i][j], 0, 0, 0);
-            });
-            return;
-        }
         const uint16_t *X = reinterpret_cast<const uint16_t *>(S);
-        if constexpr (WT == ARIA_WF16) {
-            /* fp16 weights: both operands straight from LDS, the same k order as the
-             * activation fragments of the packed paths */
-            const uint16_t *Wr = reinterpret_cast<const uint16_t *>(S + St::A);
-            static_for<4>([&](auto KS) __attribute__((always_inline)) {
-                constexpr int ks = decltype(KS)::value;
-                half8_t xf[FM], wf[FN];
-#pragma unroll
-                for (int i = 0; i < FM; i++) xf[i] = *reinterpret_cast<const half8_t *>(&X[xo(i * 32 + lrow, 4 * lh + ks)]);
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-                    wf[j] = *reinterpret_cast<const half8_t *>(&Wr[xo(rbase + 32 * j + lrow, 4 * lh + ks)]);
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], xf[i], acc[i][j], 0, 0, 0);
-            });
-            return;
-        } else {
-        WSt<WT, FN> ws;
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int r = rbase + 32 * j + lrow;
-            if constexpr (WT == ARIA_WQ8) {
-                const uint8_t *row = S + St::A + r * 64;
-                const uint4 u0 = *reinterpret_cast<const uint4 *>(row + 16 * ((2 * lh) ^ ((r >> 2) & 3)));
-                const uint4 u1 = *reinterpret_cast<const uint4 *>(row + 16 * ((2 * lh + 1) ^ ((r >> 2) & 3)));
-                ws.w[j][0] = u0.x; ws.w[j][1] = u0.y; ws.w[j][2] = u0.z; ws.w[j][3] = u0.w;
-                ws.w[j][4] = u1.x; ws.w[j][5] = u1.y; ws.w[j][6] = u1.z; ws.w[j][7] = u1.w;
-            } else {
-                const uint4 u = *reinterpret_cast<const uint4 *>(S + St::A + r * 32 + 16 * lh);
-                const int slot = FN == 2 ? (32 * j + lrow) : lrow;
-                const uint2 pr = *reinterpret_cast<const uint2 *>(S + St::A + St::WQ + 1024 * wave + 16 * slot + 8 * lh);
-                ws.w[j][0] = u.x; ws.w[j][1] = u.y; ws.w[j][2] = u.z; ws.w[j][3] = u.w;
-                ws.w[j][4] = pr.x; ws.w[j][5] = pr.y;
-            }
-        }
+        /* W8A8: lane half h covers k in [64 h, 64 h + 64) of the 128-k tile and step ks its 16
+         * k at 64 h + 16 ks on both sides (the int32 sums are exact, so any common order gives
+         * the same bits); fp16: 8 k at 32 h + 8 ks, the order of the packed paths */
+        auto afrag = [&](int i, int ks) __attribute__((always_inline)) {
+            return *reinterpret_cast<const FragT *>(&X[xo(i * 32 + lrow, 4 * lh + ks)]);
+        };
+        WSt<WT == ARIA_WQ4 ? ARIA_WQ4 : ARIA_WQ8, FN> ws;
         QOff f[FN];
+        if constexpr (WT == ARIA_WQ8 || WT == ARIA_WQ4) {
 #pragma unroll
-        for (int j = 0; j < FN; j++) f[j] = qoff<WT, FN>(ws, j);
-        half8_t xa[FM], xn[FM], wa[FN], wn[FN];
+            for (int j = 0; j < FN; j++) {
+                const int r = rbase + 32 * j + lrow;     /* weight row of the tile */
+                if constexpr (WT == ARIA_WQ8) {
+                    const uint8_t *row = S + St::A + r * 64;
+                    const uint4 u0 = *reinterpret_cast<const uint4 *>(row + 16 * ((2 * lh) ^ ((r >> 2) & 3)));
+                    const uint4 u1 = *reinterpret_cast<const uint4 *>(row + 16 * ((2 * lh + 1) ^ ((r >> 2) & 3)));
+                    ws.w[j][0] = u0.x; ws.w[j][1] = u0.y; ws.w[j][2] = u0.z; ws.w[j][3] = u0.w;
+                    ws.w[j][4] = u1.x; ws.w[j][5] = u1.y; ws.w[j][6] = u1.z; ws.w[j][7] = u1.w;
+                } else {
+                    const uint4 u = *reinterpret_cast<const uint4 *>(S + St::A + r * 32 + 16 * lh);
+                    /* row r's [min, step] pairs sit in the 1 KB area of the wave that moved them,
+                     * r / (32 FN), at slot r % (32 FN) */
+                    const int dw = r / (32 * FN), slot = r % (32 * FN);
+                    const uint2 pr = *reinterpret_cast<const uint2 *>(S + St::A + St::WQ + 1024 * dw + 16 * slot + 8 * lh);
+                    ws.w[j][0] = u.x; ws.w[j][1] = u.y; ws.w[j][2] = u.z; ws.w[j][3] = u.w;
+                    ws.w[j][4] = pr.x; ws.w[j][5] = pr.y;
+                }
+            }
 #pragma unroll
-        for (int i = 0; i < FM; i++) xa[i] = *reinterpret_cast<const half8_t *>(&X[xo(i * 32 + lrow, 4 * lh)]);
+            for (int j = 0; j < FN; j++) f[j] = qoff<WT == ARIA_WQ4 ? ARIA_WQ4 : ARIA_WQ8, FN>(ws, j);
+        }
+        auto bfrag = [&](int j, int ks) __attribute__((always_inline)) {
+            if constexpr (WT == ARIA_WF16 || WT == ARIA_WI8) {
+                const uint16_t *Wr = reinterpret_cast<const uint16_t *>(S + St::A);
+                return *reinterpret_cast<const FragT *>(&Wr[xo(rbase + 32 * j + lrow, 4 * lh + ks)]);
+            } else {
+                return wfrag<WT, FN>(ws, j, ks, magic, f[j]);
+            }
+        };
+        FragT xa[FM], xn[FM], wa[FN], wn[FN];
 #pragma unroll
-        for (int j = 0; j < FN; j++) wa[j] = wfrag<WT, FN>(ws, j, 0, magic, f[j]);
+        for (int i = 0; i < FM; i++) xa[i] = afrag(i, 0);
+#pragma unroll
+        for (int j = 0; j < FN; j++) wa[j] = bfrag(j, 0);
+        __builtin_amdgcn_sched_barrier(0);
         static_for<4>([&](auto KS) __attribute__((always_inline)) {
             constexpr int ks = decltype(KS)::value;
             if constexpr (ks < 3) {
 #pragma unroll
-                for (int i = 0; i < FM; i++)
-                    xn[i] = *reinterpret_cast<const half8_t *>(&X[xo(i * 32 + lrow, 4 * lh + ks + 1)]);
+                for (int i = 0; i < FM; i++) xn[i] = afrag(i, ks + 1);
 #pragma unroll
-                for (int j = 0; j < FN; j++) wn[j] = wfrag<WT, FN>(ws, j, ks + 1, magic, f[j]);
+                for (int j = 0; j < FN; j++) wn[j] = bfrag(j, ks + 1);
             }
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[j], xa[i], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < FN; j++) {
+                    if constexpr (WT == ARIA_WI8)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wa[j], xa[i], acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wa[j], xa[i], acc[i][j], 0, 0, 0);
+                }
             if constexpr (ks < 3) {
+                pin();
 #pragma unroll
                 for (int i = 0; i < FM; i++) xa[i] = xn[i];
 #pragma unroll
                 for (int j = 0; j < FN; j++) wa[j] = wn[j];
             }
         });
-        }
         });
     };
 
@@ -429,14 +429,14 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
     /* every wave is past its last fragment read (the last step's barrier): the stages hold the
      * epilogue staging */
     float *E = reinterpret_cast<float *>(smem + wave * EPI_WAVE);
-    epilogue<FM, FN, WT, MODE, GELU, AccT>(a, acc, E, lane, m0, n0 + wave * 32 * FN);
+    epilogue<FM, FN, WT, MODE, GELU, AccT>(a, acc, E, lane, m0, n0 + rbase);
 }
 
 /* NST = 0: three stages where they fit the LDS share of MINB workgroups, else two */
 template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int KSPL = 1, int NS = 1, int NST = 0>
 static void launch_big_m(const QArgs &a, hipStream_t s) {
     constexpr int BM = 32 * FM, BN = 128 * FN;
-    constexpr int NSTA = NST ? NST : (3 * KSPL * NS * Stage<WT, FM, FN>::BYTES <= (MINB == 1 ? 160 : 80) * 1024 ? 3 : 2);
+    constexpr int NSTA = NST ? NST : (3 * KSPL * NS * Stage<WT, FM, FN>::BYTES <= 160 * 1024 / MINB ? 3 : 2);
     const int MT = (a.M + BM - 1) / BM, NTN = (a.N + BN - 1) / BN, T = MT * NTN;
     const int grid = ((T + 7) / 8) * 8;
     hipLaunchKernelGGL((k_qgemm_big<WT, FM, FN, MODE, GELU, MINB, NS, NSTA, KSPL>), dim3(grid), dim3(256 * KSPL), 0, s,

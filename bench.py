@@ -120,6 +120,8 @@ def parse():
     ap.add_argument("--sets", type=int, default=4, help="rotating buffer sets (cache defeat)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-dit", action="store_true", help="skip the 24-block DiT stack leg")
+    ap.add_argument("--c2-only", action="store_true",
+                    help="only the C2 legs (the step, per-op loops, ceilings): for a kernel trace of them")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: each C2 op a few times with no events in between, plus one "
                          "256 MiB device-to-device copy whose FETCH/WRITE counters calibrate the others")
@@ -129,6 +131,9 @@ def parse():
     ap.add_argument("--micro", action="store_true",
                     help="only the issue-rate and bandwidth probes (aria_amd/libaria_probe.so, built from "
                          "csrc/probe_micro.hip): fp16 MFMA, fp32 FMA, exp2, reciprocal, LDS and L1 reads")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="only the K-sweep of the config-3 dequant GEMMs (M = 2592, N 4096 / 1024, K 512-4096, "
+                         "Q8 / Q4, fp16 activations) with the fit t = t0 + c * K / 64 per (weights, N)")
     ap.add_argument("--vendor", action="store_true",
                     help="only the vendor-library reference points: PyTorch's fp16 GEMM (hipBLASLt) and "
                          "scaled_dot_product_attention at this build's GEMM and attention shapes")
@@ -330,6 +335,9 @@ def main():
     print(f"[bench] device: {aria_amd.device_info()}", file=sys.stderr, flush=True)
 
     rng = np.random.default_rng(SEED)
+    if args.gemm_sweep:
+        print(json.dumps({"gemm_sweep": gemm_sweep_leg(L, chk, DeviceArray, Timer, stream, rng)}), flush=True)
+        return
     if args.micro:
         print(json.dumps({"micro": micro_leg(L, chk, DeviceArray, Timer, stream)}), flush=True)
         return
@@ -513,17 +521,19 @@ def main():
         ops_report[name] = {"us": round(ms * 1e3, 2), "GB/s": round(byt / (ms * 1e-3) / 1e9, 1), "bytes": byt}
     del d_W
 
-    # C3: Q8 / Q4 dequant-on-use GEMMs at M = 2592 (fp32 activations, as aria_linear_q8/q4 take)
-    gemm = gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps)
     xpool.free(); opool.free()
     for d in spool:
         d.free()
-    # C4: one q4 DiT block at T = 1296, batch 2
-    block = block_leg(DeviceArray, time_loop, stream, rng, reps)
-    # C5: 24-block q4 stack x 8 steps, graph replay vs inline, and the device sampler
-    dit = None if args.no_dit else dit_leg(DeviceArray, Timer, L, chk, stream, rng)
-    # F4: the device small-music decoder at 10 s and 60 s of audio
-    dec = dec_leg(DeviceArray, Timer, rng)
+    gemm = block = dit = dec = None
+    if not args.c2_only:
+        # C3: Q8 / Q4 dequant-on-use GEMMs at M = 2592 (fp32 activations, as aria_linear_q8/q4 take)
+        gemm = gemm_leg(L, chk, DeviceArray, time_loop, stream, rng, reps)
+        # C4: one q4 DiT block at T = 1296, batch 2
+        block = block_leg(DeviceArray, time_loop, stream, rng, reps)
+        # C5: 24-block q4 stack x 8 steps, graph replay vs inline, and the device sampler
+        dit = None if args.no_dit else dit_leg(DeviceArray, Timer, L, chk, stream, rng)
+        # F4: the device small-music decoder at 10 s and 60 s of audio
+        dec = dec_leg(DeviceArray, Timer, rng)
 
     dom = max(OPS, key=lambda o: ops_report[o]["us"])
     dom_us = ops_report[dom]["us"]
@@ -557,7 +567,7 @@ def main():
         "ops": ops_report,
         "ceiling": ceiling,
         "gemm": gemm,
-        "block_us": block["gelu"]["us"],
+        "block_us": block["gelu"]["us"] if block else None,
         "block": block,
         "dit": dit,
         "dec": dec,
@@ -647,6 +657,54 @@ def ceiling_leg(L, chk, DeviceArray, time_graph, stream, xpool, opool, nslot, n_
             ms, mn = time_graph(fn, reps)
             out[key + tag] = {"us": round(ms * 1e3, 2), "us_min": round(mn * 1e3, 2),
                               "GB/s": round(byt / (ms * 1e-3) / 1e9, 1), "bytes": byt}
+    return out
+
+
+def gemm_sweep_leg(L, chk, DeviceArray, Timer, stream, rng, reps=20):
+    """Split each config-3 GEMM's time into a fixed part and a part per 64-deep K-tile: at
+    M = 2592 rows and N = 4096 / 1024 weight rows, K = 512, 1024, 2048, 4096, Q8 and Q4
+    weights ~N(0, 0.02) packed on the device, fp16 activations ~N(0, 1), fp32 output, the
+    tile configuration the library picks for the shape. Each point is the fastest of 5
+    trials of `reps` back-to-back launches (HIP events on the stream, 4 rotating activation
+    buffers, 3 untimed launches first). Per (weights, N) a least-squares line
+    t = t0 + c * (K / 64) over the four points: t0 is what a launch costs whatever its depth
+    (launch, pipeline fill, the epilogue and its stores), c the cost of one more K-tile."""
+    M = B * S
+    out = {"M": M, "points_us": {}, "fit": {}}
+    for N in (4096, 1024):
+        pts = {0: [], 1: []}
+        for K in (512, 1024, 2048, 4096):
+            dW = DeviceArray.from_host((0.02 * rng.standard_normal((N, K))).astype(np.float32))
+            dx = [DeviceArray.from_host(rng.standard_normal((M, K)).astype(np.float16)) for _ in range(4)]
+            dy = DeviceArray((M, N))
+            dq8, ds8 = DeviceArray((N, K), np.int8), DeviceArray(N, np.float32)
+            dq4, ds4 = DeviceArray((N, K // 2), np.uint8), DeviceArray((N, 2 * K // 32), np.float32)
+            chk(L.aria_hip_q8_quant_dev(dq8.p, ds8.p, dW.p, N, K, stream))
+            chk(L.aria_hip_q4_quant_dev(dq4.p, ds4.p, dW.p, N, K, stream))
+            for wt, dq, ds in ((0, dq8, ds8), (1, dq4, ds4)):
+                fn = (lambda i, wt=wt, dq=dq, ds=ds:
+                      L.aria_hip_qlinear_dev(dy.p, 0, dx[i % 4].p, 1, wt, dq.p, ds.p, None, M, K, N, stream))
+                for i in range(3):
+                    chk(fn(i))
+                best = 1e30
+                for _ in range(5):
+                    tm = Timer(stream)
+                    tm.start()
+                    for i in range(reps):
+                        chk(fn(i))
+                    best = min(best, tm.stop() / reps * 1e3)
+                name = "q8" if wt == 0 else "q4"
+                out["points_us"][f"{name}_N{N}_K{K}"] = round(best, 2)
+                pts[wt].append((K / 64.0, best))
+            for d in dx + [dW, dy, dq8, ds8, dq4, ds4]:
+                d.free()
+        for wt in (0, 1):
+            xs = np.array([p[0] for p in pts[wt]]); ys = np.array([p[1] for p in pts[wt]])
+            c, t0 = np.polyfit(xs, ys, 1)
+            out["fit"][f"{'q8' if wt == 0 else 'q4'}_N{N}"] = {
+                "t0_us": round(float(t0), 2), "c_us_per_ktile": round(float(c), 3),
+                "t0_share_at_K1024": round(float(t0 / (t0 + 16 * c)), 3),
+                "max_resid_us": round(float(np.max(np.abs(ys - (t0 + c * xs)))), 2)}
     return out
 
 
