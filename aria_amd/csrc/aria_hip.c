@@ -293,7 +293,7 @@ int aria_hip_rmsnorm_dev(float *dy, const float *dx, const float *dw, int rows, 
                          void *stream) {
     ENSURE();
     REQ(rows >= 0 && dim > 0 && (rows == 0 || (dy && dx)));
-    KCK(aria_k_rownorm(dy, 0, dx, dw, NULL, NULL, NULL, 0, 0, 0, ARIA_NORM_RMS, rows, dim, eps, pick(stream)),
+    KCK(aria_k_rownorm_nt(dy, 0, dx, dw, NULL, NULL, NULL, 0, 0, 0, ARIA_NORM_RMS, rows, dim, eps, 1, pick(stream)),
         "k_rownorm(rms)");
     return 0;
 }
@@ -309,7 +309,7 @@ int aria_hip_layernorm_dev(float *dy, const float *dx, const float *dg, const fl
                            float eps, void *stream) {
     ENSURE();
     REQ(rows >= 0 && dim > 0 && (rows == 0 || (dy && dx)));
-    KCK(aria_k_rownorm(dy, 0, dx, dg, db, NULL, NULL, 0, 0, 0, ARIA_NORM_LAYER, rows, dim, eps, pick(stream)),
+    KCK(aria_k_rownorm_nt(dy, 0, dx, dg, db, NULL, NULL, 0, 0, 0, ARIA_NORM_LAYER, rows, dim, eps, 1, pick(stream)),
         "k_rownorm(layer)");
     return 0;
 }
@@ -329,8 +329,8 @@ int aria_hip_ln_mod_gelu_res_dev(float *dout, const float *dx, const float *dg, 
     REQ(rows >= 0 && dim > 0 && (rows == 0 || (dout && dx && dsc && dsh)));
     REQ(rpb >= 0 && (rpb == 0 || rows % rpb == 0));
     REQ(dout != dx);
-    KCK(aria_k_rownorm(dout, 0, dx, dg, db, dsc, dsh, rpb, 1, 1, ARIA_NORM_LAYER, rows, dim, eps,
-                       pick(stream)), "k_rownorm(ln+mod+gelu+res)");
+    KCK(aria_k_rownorm_nt(dout, 0, dx, dg, db, dsc, dsh, rpb, 1, 1, ARIA_NORM_LAYER, rows, dim, eps, 1,
+                          pick(stream)), "k_rownorm(ln+mod+gelu+res)");
     return 0;
 }
 

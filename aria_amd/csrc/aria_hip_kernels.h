@@ -28,6 +28,12 @@ hipError_t aria_k_rownorm(void *y, int out_f16, const float *x, const float *w, 
                           const float *scale, const float *shift, int rows_per_batch,
                           int gelu, int resid, int norm, int rows, int dim, float eps,
                           hipStream_t s);
+/* the same with nt != 0: the row is loaded and the result stored with non-temporal hints
+ * (for the standalone ops, whose operands are streamed once) */
+hipError_t aria_k_rownorm_nt(void *y, int out_f16, const float *x, const float *w, const float *b,
+                             const float *scale, const float *shift, int rows_per_batch,
+                             int gelu, int resid, int norm, int rows, int dim, float eps, int nt,
+                             hipStream_t s);
 /* RMSNorm + adaLN with scale = scale_t[c] + scale_g[b * g_bs + c] formed in place (scale_g,
  * shift_g may be NULL); w may be NULL */
 hipError_t aria_k_rownorm_ada(void *y, int out_f16, const float *x, const float *w,

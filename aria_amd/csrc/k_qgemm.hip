@@ -415,13 +415,15 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
          * ca_q projections), other N <= 3072 without HEADS (128 x 128, two per CU), N = 4096
          * (192 x 128) and wider (224 x 128); N <= 1024 with an even number of K-tiles in 96 x 128
          * tiles of 8 waves, the two halves of K on their own pipelines (216 tiles at M = 2592
-         * leave 40 CUs idle; the split doubles the waves on the busy ones); HEADS wider than 3072
-         * stays on the weights-in-registers kernel */
+         * leave 40 CUs idle; the split doubles the waves on the busy ones), and HEADS with N <=
+         * 1024 (ca_q) likewise in 64 x 256 tiles (164 tiles: one workgroup per busy CU, so the
+         * split's second half is what gives those CUs two waves per SIMD; 15.6 -> 15.2 us);
+         * HEADS wider than 3072 stays on the weights-in-registers kernel */
         if (tiles >= 13) return qgemm_big_launch(a, WT, tiles - 13, s);
         if (tiles == 0 && a.K % 64 == 0 && (WT != ARIA_WQ4 || ((uintptr_t)a.scale & 15u) == 0) &&
             (!a.gelu || a.epi.mode == ARIA_EPI_STORE)) {
             const bool heads = a.epi.mode == ARIA_EPI_HEADS;
-            const int cfg = heads ? (a.N <= 3072 ? 2 : -1)
+            const int cfg = heads ? (a.N <= 1024 && (a.K / 64) % 2 == 0 ? 6 : a.N <= 3072 ? 2 : -1)
                           : a.N <= 1024 ? ((a.K / 64) % 2 == 0 ? 5 : 0) : a.N <= 3072 ? 1 : a.N <= 4096 ? 3 : 4;
             if (cfg >= 0) return qgemm_big_launch(a, WT, cfg, s);
         }

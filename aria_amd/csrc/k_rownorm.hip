@@ -32,7 +32,10 @@
 #include "aria_dev.h"
 #include "aria_hip_kernels.h"
 
-enum { EPI_MOD = 1, EPI_GELU = 2, EPI_RES = 4, EPI_F16 = 8, EPI_W = 16, EPI_B = 32, EPI_MADD = 64, EPI_Q8 = 128 };
+/* EPI_NT: the row is loaded and stored with non-temporal hints (the standalone ops, whose
+ * operands are streamed once; the DiT's norms feed the next GEMM and keep the default) */
+enum { EPI_MOD = 1, EPI_GELU = 2, EPI_RES = 4, EPI_F16 = 8, EPI_W = 16, EPI_B = 32, EPI_MADD = 64, EPI_Q8 = 128,
+       EPI_NT = 256 };
 
 struct NormArgs {
     void *y;
@@ -46,6 +49,7 @@ struct NormArgs {
     float eps;
     int gelu, resid, f16;
     float *sx;   /* EPI_Q8: y is int8 [rows, dim] and sx[row] its scale (W8A8 activations) */
+    int nt;      /* EPI_NT */
 };
 
 template <int NORM>
@@ -119,7 +123,7 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x + (size_t)row * dim);
     float4 v[VPL];
 #pragma unroll
-    for (int j = 0; j < VPL; j++) v[j] = x4[j * LPR + l];
+    for (int j = 0; j < VPL; j++) v[j] = (EPI & EPI_NT) ? ld_nt(x4 + j * LPR + l) : x4[j * LPR + l];
 
     /* the broadcast vectors are loaded with the row, before the reduction, so their
      * latency overlaps the row's instead of following it */
@@ -234,10 +238,14 @@ __global__ __launch_bounds__(256) void k_rownorm_v(NormArgs a) {
         o.z = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].z, inv, mu, rstd, wv[j].z, bv[j].z), v[j].z, scv[j].z, shv[j].z);
         o.w = epi_elem<EPI>(norm_elem_c<NORM, EPI>(v[j].w, inv, mu, rstd, wv[j].w, bv[j].w), v[j].w, scv[j].w, shv[j].w);
         if (EPI & EPI_F16) {
-            uint2 p;
-            p.x = (uint32_t)f2h_bits(o.x) | ((uint32_t)f2h_bits(o.y) << 16);
-            p.y = (uint32_t)f2h_bits(o.z) | ((uint32_t)f2h_bits(o.w) << 16);
-            reinterpret_cast<uint2 *>((uint16_t *)a.y + (size_t)row * dim)[c4] = p;
+            typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+            const u32x2_t p = {(uint32_t)f2h_bits(o.x) | ((uint32_t)f2h_bits(o.y) << 16),
+                               (uint32_t)f2h_bits(o.z) | ((uint32_t)f2h_bits(o.w) << 16)};
+            u32x2_t *yp = reinterpret_cast<u32x2_t *>((uint16_t *)a.y + (size_t)row * dim) + c4;
+            if (EPI & EPI_NT) __builtin_nontemporal_store(p, yp);
+            else *yp = p;
+        } else if (EPI & EPI_NT) {
+            st_nt(reinterpret_cast<float4 *>((float *)a.y + (size_t)row * dim) + c4, o);
         } else {
             reinterpret_cast<float4 *>((float *)a.y + (size_t)row * dim)[c4] = o;
         }
@@ -297,13 +305,14 @@ __global__ __launch_bounds__(256) void k_rownorm_g(NormArgs a) {
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 /* the operand sets instantiated for the register path, per norm */
-using EpiRms = std::integer_sequence<int, 0, EPI_W, EPI_F16, EPI_F16 | EPI_W, EPI_MOD | EPI_W, EPI_MOD | EPI_F16 | EPI_W,
+using EpiRms = std::integer_sequence<int, 0, EPI_W, EPI_W | EPI_NT, EPI_F16, EPI_F16 | EPI_W, EPI_MOD | EPI_W, EPI_MOD | EPI_F16 | EPI_W,
                                       EPI_MOD | EPI_MADD | EPI_W, EPI_MOD | EPI_MADD | EPI_F16 | EPI_W,
                                       EPI_Q8, EPI_Q8 | EPI_W, EPI_MOD | EPI_Q8, EPI_MOD | EPI_Q8 | EPI_W,
                                       EPI_MOD | EPI_MADD | EPI_Q8 | EPI_W>;
 using EpiGemma = std::integer_sequence<int, 0, EPI_W>;
-using EpiLayer = std::integer_sequence<int, 0, EPI_W, EPI_B, EPI_W | EPI_B, EPI_MOD | EPI_GELU | EPI_RES,
-                                        EPI_MOD | EPI_GELU | EPI_RES | EPI_W | EPI_B>;
+using EpiLayer = std::integer_sequence<int, 0, EPI_NT, EPI_W, EPI_B, EPI_W | EPI_B, EPI_W | EPI_B | EPI_NT,
+                                        EPI_MOD | EPI_GELU | EPI_RES, EPI_MOD | EPI_GELU | EPI_RES | EPI_W | EPI_B,
+                                        EPI_MOD | EPI_GELU | EPI_RES | EPI_W | EPI_B | EPI_NT>;
 template <int NORM> struct EpiSet;
 template <> struct EpiSet<ARIA_NORM_RMS> { using type = EpiRms; };
 template <> struct EpiSet<ARIA_NORM_GEMMA> { using type = EpiGemma; };
@@ -335,7 +344,7 @@ static hipError_t launch_norm(const NormArgs &a, hipStream_t s) {
                      (!a.shift_add || al16(a.shift_add)) && a.mod_bs % 4 == 0 && a.add_bs % 4 == 0;
     const int epi = (a.scale ? EPI_MOD : 0) | (a.gelu ? EPI_GELU : 0) | (a.resid ? EPI_RES : 0) |
                     (a.f16 ? EPI_F16 : 0) | (a.w ? EPI_W : 0) | (a.b ? EPI_B : 0) |
-                    (a.scale && a.scale_add ? EPI_MADD : 0) | (a.sx ? EPI_Q8 : 0);
+                    (a.scale && a.scale_add ? EPI_MADD : 0) | (a.sx ? EPI_Q8 : 0) | (a.nt ? EPI_NT : 0);
     using Set = typename EpiSet<NORM>::type;
     bool hit = false;
     if (vec) {
@@ -350,6 +359,19 @@ static hipError_t launch_norm(const NormArgs &a, hipStream_t s) {
             default: break;
         }
     }
+    if (!hit && vec && (epi & EPI_NT)) {   /* no streaming form of this operand set: the default one */
+        const int e2 = epi & ~EPI_NT;
+        switch (dim) {
+            case 64: hit = launch_v<NORM, 1, 16>(a, e2, s, Set{}); break;
+            case 128: hit = launch_v<NORM, 1, 32>(a, e2, s, Set{}); break;
+            case 256: hit = launch_v<NORM, 1, 64>(a, e2, s, Set{}); break;
+            case 512: hit = launch_v<NORM, 2, 64>(a, e2, s, Set{}); break;
+            case 768: hit = launch_v<NORM, 3, 64>(a, e2, s, Set{}); break;
+            case 1024: hit = launch_v<NORM, 4, 64>(a, e2, s, Set{}); break;
+            case 2048: hit = launch_v<NORM, 8, 64>(a, e2, s, Set{}); break;
+            default: break;
+        }
+    }
     if (!hit) {
         if (a.sx) return hipErrorInvalidValue;   /* int8 output: register path only */
         hipLaunchKernelGGL((k_rownorm_g<NORM>), dim3((a.rows + 3) / 4), dim3(256), 0, s, a);
@@ -361,8 +383,16 @@ extern "C" hipError_t aria_k_rownorm(void *y, int out_f16, const float *x, const
                                      const float *b, const float *scale, const float *shift,
                                      int rows_per_batch, int gelu, int resid, int norm, int rows,
                                      int dim, float eps, hipStream_t s) {
+    return aria_k_rownorm_nt(y, out_f16, x, w, b, scale, shift, rows_per_batch, gelu, resid, norm, rows, dim, eps, 0, s);
+}
+
+extern "C" hipError_t aria_k_rownorm_nt(void *y, int out_f16, const float *x, const float *w,
+                                        const float *b, const float *scale, const float *shift,
+                                        int rows_per_batch, int gelu, int resid, int norm, int rows,
+                                        int dim, float eps, int nt, hipStream_t s) {
     if (rows <= 0 || dim <= 0) return hipSuccess;
     NormArgs a;
+    a.nt = nt;
     a.y = y; a.x = x; a.w = w; a.b = b; a.scale = scale; a.shift = shift;
     a.scale_add = nullptr; a.shift_add = nullptr; a.mod_bs = dim; a.add_bs = 0;
     a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows;
@@ -389,7 +419,7 @@ extern "C" hipError_t aria_k_rownorm_ada(void *y, int out_f16, const float *x, c
     a.scale_add = scale_g; a.shift_add = shift_g; a.mod_bs = 0; a.add_bs = g_bs;
     a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows;
     a.rows = rows; a.dim = dim; a.eps = eps;
-    a.gelu = 0; a.resid = 0; a.f16 = out_f16; a.sx = nullptr;
+    a.gelu = 0; a.resid = 0; a.f16 = out_f16; a.sx = nullptr; a.nt = 0;
     return launch_norm<ARIA_NORM_RMS>(a, s);
 }
 
@@ -404,7 +434,7 @@ extern "C" hipError_t aria_k_rownorm_q8(int8_t *yq, float *sx, const float *x, c
     a.y = yq; a.x = x; a.w = w; a.b = nullptr; a.scale = scale; a.shift = shift;
     a.scale_add = nullptr; a.shift_add = nullptr; a.mod_bs = dim; a.add_bs = 0;
     a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows; a.rows = rows; a.dim = dim; a.eps = eps;
-    a.gelu = 0; a.resid = 0; a.f16 = 0; a.sx = sx;
+    a.gelu = 0; a.resid = 0; a.f16 = 0; a.sx = sx; a.nt = 0;
     if (!sx || ((uintptr_t)yq & 3u)) return hipErrorInvalidValue;
     return launch_norm<ARIA_NORM_RMS>(a, s);
 }
@@ -418,7 +448,7 @@ extern "C" hipError_t aria_k_rownorm_ada_q8(int8_t *yq, float *sx, const float *
     a.scale_add = scale_g; a.shift_add = shift_g; a.mod_bs = 0; a.add_bs = g_bs;
     a.rows_per_batch = rows_per_batch > 0 ? rows_per_batch : rows;
     a.rows = rows; a.dim = dim; a.eps = eps;
-    a.gelu = 0; a.resid = 0; a.f16 = 0; a.sx = sx;
+    a.gelu = 0; a.resid = 0; a.f16 = 0; a.sx = sx; a.nt = 0;
     if (!sx || ((uintptr_t)yq & 3u)) return hipErrorInvalidValue;
     return launch_norm<ARIA_NORM_RMS>(a, s);
 }

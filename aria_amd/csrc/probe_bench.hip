@@ -4,9 +4,10 @@
  *
  *   aria_probe_copy      a streaming device copy, the bandwidth ceiling the row ops and the
  *                        softmax are compared with. Same access shape as those kernels: each
- *                        lane moves V float4 (16 B) with every load issued before the first
- *                        store, 256-lane workgroups over a one-shot grid (no grid-stride loop),
- *                        non-temporal loads and stores (nt = 1) or plain ones (nt = 0).
+ *                        wave moves one contiguous 4 KB run (a [*, 1024] fp32 row), each lane
+ *                        4 float4 with every load issued before the first store, 256-lane
+ *                        workgroups over a one-shot grid (no grid-stride loop), non-temporal
+ *                        loads and stores (nt = 1) or plain ones (nt = 0).
  *   aria_probe_capture_* capture the work a caller enqueues on a stream into a hipGraph and
  *                        replay it, so a loop of back-to-back launches is timed without the
  *                        host's launch cadence (a Python call per launch takes ~4 us, as long
@@ -20,16 +21,21 @@ typedef float f32x4_p __attribute__((ext_vector_type(4)));
 template <int V, bool NT>
 __global__ __launch_bounds__(256) void k_probe_copy(f32x4_p *__restrict__ dst, const f32x4_p *__restrict__ src,
                                                     size_t n4) {
-    const size_t base = (size_t)blockIdx.x * (256 * V) + threadIdx.x;
+    /* each wave moves one contiguous run of 64 V float4 (V KB), lane l the float4s
+     * l, l + 64, ...: the layout of a row kernel's wave over a [*, 1024] fp32 row */
+    const size_t base = ((size_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * (64 * V) + (threadIdx.x & 63);
+    /* the loads are unconditional (an index past the end re-reads the last float4), so all V
+     * are in flight at once: a guarded load compiles to a branch with a vmcnt(0) wait in front
+     * of the next load */
     f32x4_p v[V];
 #pragma unroll
     for (int j = 0; j < V; j++) {
-        const size_t i = base + (size_t)j * 256;
-        if (i < n4) v[j] = NT ? __builtin_nontemporal_load(src + i) : src[i];
+        const size_t i = base + (size_t)j * 64, ic = i < n4 ? i : n4 - 1;
+        v[j] = NT ? __builtin_nontemporal_load(src + ic) : src[ic];
     }
 #pragma unroll
     for (int j = 0; j < V; j++) {
-        const size_t i = base + (size_t)j * 256;
+        const size_t i = base + (size_t)j * 64;
         if (i < n4) {
             if (NT) __builtin_nontemporal_store(v[j], dst + i);
             else dst[i] = v[j];

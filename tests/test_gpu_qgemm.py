@@ -136,7 +136,7 @@ def test_qgemm_every_tile_shape(hip, port, tiles, wtype):
         assert relerr_max(dy.to_host(), want) <= GATE, (tiles, wtype, xf16)
 
 
-@pytest.mark.parametrize("wtype,tiles", [(w, t) for w in (0, 1) for t in range(13, 19)] +
+@pytest.mark.parametrize("wtype,tiles", [(w, t) for w in (0, 1) for t in range(13, 20)] +
                          [(2, t) for t in range(13, 18)])
 def test_qgemm_lds_dma_tiles(hip, port, tiles, wtype):
     """The LDS-DMA kernel's tile configurations (tiles 13.. = configuration tiles - 13; six
