@@ -568,9 +568,10 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
  *   3: 192 x 128, two per CU in two stages: N > 3072 (ff_in N = 4096: 29.3 -> 22.7 us;
  *      the GLU ff_in N = 8192: 61.4 -> 49.6 us)
  *   4: 96 x 128 in 8-wave workgroups (the K range split, two stages each): N <= 1024 with
- *      K >= 2048 (ff_out: 23.6 -> 21.7 us) */
-#define BIG_I8_CFGS(X) X(0, 2, 1, 2, 1) X(1, 2, 2, 2, 1) X(2, 4, 1, 2, 1) X(3, 6, 1, 2, 1) X(4, 3, 1, 1, 2)
-int qgemm_big_i8_ncfg() { return 5; }
+ *      K >= 2048 (ff_out: 23.6 -> 21.7 us)
+ *   5: 64 x 256 in 8-wave workgroups, the K range split: HEADS with N <= 1024 (ca_q) */
+#define BIG_I8_CFGS(X) X(0, 2, 1, 2, 1) X(1, 2, 2, 2, 1) X(2, 4, 1, 2, 1) X(3, 6, 1, 2, 1) X(4, 3, 1, 1, 2) X(5, 2, 2, 1, 2)
+int qgemm_big_i8_ncfg() { return 6; }
 
 hipError_t qgemm_big_i8_launch(const QArgs &a, int cfg, hipStream_t s) {
     if (a.K % 128 || (a.gelu && a.epi.mode != ARIA_EPI_STORE)) return hipErrorInvalidValue;
