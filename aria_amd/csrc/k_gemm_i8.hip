@@ -357,13 +357,15 @@ extern "C" hipError_t aria_k_gemm_i8_t(void *y, int y_f16, const int8_t *xq, con
     const bool heads = a.epi.mode == ARIA_EPI_HEADS;
     if (fm <= 0 && K % 128 == 0 && (!heads || N <= 3072)) {
         /* the LDS-DMA kernel (k_qgemm_big.hip) at every DiT shape: HEADS in 64 x 256, N <= 1024
-         * in 64 x 128, N <= 3072 in 128 x 128, wider in 192 x 128 (two workgroups per CU); N <= 1024
+         * in 64 x 128, N <= 3072 in 128 x 128, wider in 192 x 128 (two workgroups per CU), except
+         * N = 4096 in 192 x 256 tiles of 8 waves sharing the activation tile (ff_in 24.3 -> 23.6 us
+         * with GELU, the same bits); N <= 1024
          * with K >= 2048 (ff_out) in 96 x 128 tiles of 8 waves, the K range split between two
          * pipelines (23.6 -> 21.7 us at K = 4096; at K = 1024 the split measured 6 % slower);
          * HEADS with N <= 1024 (ca_q: 164 tiles, one workgroup per busy CU) in 64 x 256 tiles
          * with the split (14.0 -> 12.7 us, the same bits: int32 sums are exact) */
         return qgemm_big_i8_launch(a, heads ? ((N <= 1024 && (K / 128) % 2 == 0) ? 5 : 1) : N <= 1024 ? ((K >= 2048 && (K / 128) % 2 == 0) ? 4 : 0)
-                                                    : N <= 3072 ? 2 : 3, s);
+                                                    : N <= 3072 ? 2 : N <= 4096 ? 6 : 3, s);
     }
     if (fm <= 0) {
         /* tile rows, from a sweep at M = 2592 (fm: 1..4 = 32..128 rows): 128 rows when those

@@ -413,7 +413,8 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
          * or picked for the shapes where it measured fastest: N <= 1024 without HEADS (96 x 128
          * tiles, two workgroups per CU), HEADS with N <= 3072 (64 x 256, two per CU: the qkv and
          * ca_q projections), other N <= 3072 without HEADS (128 x 128, two per CU), N = 4096
-         * (192 x 128) and wider (224 x 128); N <= 1024 with an even number of K-tiles in 96 x 128
+         * (192 x 256 in 8-wave workgroups, one per CU) and wider (224 x 128); N <= 1024 with an
+         * even number of K-tiles in 96 x 128
          * tiles of 8 waves, the two halves of K on their own pipelines (216 tiles at M = 2592
          * leave 40 CUs idle; the split doubles the waves on the busy ones), and HEADS with N <=
          * 1024 (ca_q) likewise in 64 x 256 tiles (164 tiles: one workgroup per busy CU, so the
@@ -424,7 +425,7 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
             (!a.gelu || a.epi.mode == ARIA_EPI_STORE)) {
             const bool heads = a.epi.mode == ARIA_EPI_HEADS;
             const int cfg = heads ? (a.N <= 1024 && (a.K / 64) % 2 == 0 ? 6 : a.N <= 3072 ? 2 : -1)
-                          : a.N <= 1024 ? ((a.K / 64) % 2 == 0 ? 5 : 0) : a.N <= 3072 ? 1 : a.N <= 4096 ? 3 : 4;
+                          : a.N <= 1024 ? ((a.K / 64) % 2 == 0 ? 5 : 0) : a.N <= 3072 ? 1 : a.N <= 4096 ? 7 : 4;
             if (cfg >= 0) return qgemm_big_launch(a, WT, cfg, s);
         }
         /* weights-in-registers kernel: explicit tiles 9..12 (BM = 32 * (tiles - 8)), or the pick */

@@ -117,17 +117,21 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t m0) {
  *   W8A8: [.., + 128 BN)   weights [BN][128] int8, chunk-swizzled as the activations
  *   fp16: [.., + 128 BN)   weights [BN][64] fp16, chunk-swizzled as the activations
  *   Q4: [.., + 32 BN)      nibbles [BN][32 B]
- *       [.., + 4096)       [min, step] pairs of the K-tile, 16 B per row: wave w's 64 slots
- *                          at 1024 w (FN = 1: rows 32w.. in slots 0-31, 32-63 repeat them) */
-template <int WT, int FM, int FN>
+ *       [.., + 4096 NSP)   [min, step] pairs of the K-tile, 16 B per row: wave w's 64 slots
+ *                          at 1024 w (FN = 1: rows 32w.. in slots 0-31, 32-63 repeat them)
+ * NSP = 2: 8 waves share the activation tile, each moving half as many of its slots, and
+ * own 32 FN weight rows each (BN = 256 FN). */
+template <int WT, int FM, int FN, int NSP = 1>
 struct Stage {
-    static constexpr int BM = 32 * FM, BN = 128 * FN;
+    static constexpr int BM = 32 * FM, BN = 128 * FN * NSP;
     static constexpr int A = BM * 128;
     static constexpr int WQ = (WT == ARIA_WI8 || WT == ARIA_WF16) ? BN * 128 : WT == ARIA_WQ8 ? BN * 64 : BN * 32;
-    static constexpr int WS = WT == ARIA_WQ4 ? 4096 : 0;
+    static constexpr int WS = WT == ARIA_WQ4 ? 4096 * NSP : 0;
     static constexpr int BYTES = A + WQ + WS;
+    /* activation transfers per wave and K-tile: the tile's 256 FM slots of 16 B over 4 NSP waves */
+    static constexpr int AD = FM / NSP;
     /* VMEM instructions one wave issues per K-tile */
-    static constexpr int DMA = FM + ((WT == ARIA_WI8 || WT == ARIA_WF16) ? 4 * FN : WT == ARIA_WQ8 ? 2 * FN : FN + 1);
+    static constexpr int DMA = AD + ((WT == ARIA_WI8 || WT == ARIA_WF16) ? 4 * FN : WT == ARIA_WQ8 ? 2 * FN : FN + 1);
     /* k per K-tile: 64 fp16 activations, or 128 int8 ones (W8A8), in the 128-byte rows */
     static constexpr int KK = WT == ARIA_WI8 ? 128 : 64;
 };
@@ -138,16 +142,17 @@ struct Stage {
  * LDS allow two: the second workgroup's waves cover one workgroup's barrier waits and its
  * epilogue). The tiles of an XCD are a contiguous run in M-major order (xcd_tile). Wave w
  * owns weight rows [32 FN w, 32 FN (w + 1)) and every activation row of the tile. */
-template <int WT, int FM, int FN, int MODE, bool GELU, int MINB, int NS, int NST, int KSPL>
-__global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN, int T) {
-    using St = Stage<WT, FM, FN>;   /* one 64-deep sub-tile; a pipeline stage holds NS of them */
+template <int WT, int FM, int FN, int MODE, bool GELU, int MINB, int NS, int NST, int KSPL, int NSP>
+__global__ __launch_bounds__(256 * KSPL * NSP, MINB) void k_qgemm_big(QArgs a, int NTN, int T) {
+    using St = Stage<WT, FM, FN, NSP>;   /* one 64-deep sub-tile; a pipeline stage holds NS of them */
+    static_assert(NSP == 1 || (NSP == 2 && KSPL == 1 && FM % 2 == 0), "an N split of even row blocks, K unsplit");
     constexpr int SB = NS * St::BYTES;                                 /* stage bytes */
     constexpr int PD = NST - 1;                                        /* prefetch distance */
     static_assert(NST >= 2 && NST <= 4, "two to four stages");
     constexpr int BM = St::BM, BN = St::BN;
     constexpr int EPI_STRIDE = 32 * FN * 4 + 16;
     constexpr int EPI_WAVE = 32 * EPI_STRIDE;                          /* bytes per wave */
-    static_assert(NST * SB >= 4 * EPI_WAVE, "the epilogue staging fits the stages");
+    static_assert(NST * SB >= 4 * NSP * EPI_WAVE, "the epilogue staging fits the stages");
     static_assert(KSPL == 1 || KSPL == 2, "one or two K halves");
     static_assert(KSPL * NST * SB <= 160 * 1024 / MINB, "the stages fit the LDS share of MINB workgroups");
     static_assert(KSPL == 1 || KSPL * NST * SB >= FM * FN * 16 * 256 * 4, "the second half's partial sums fit the stages");
@@ -159,7 +164,7 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
      * their partial sums join the first half's before the epilogue (fixed order) */
     const int khalf = KSPL == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
     uint8_t *const smem = smem_all + khalf * (NST * SB);
-    const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x & (256 * NSP - 1), lane = tid & 63, wave = tid >> 6;
     const int lrow = lane & 31, lh = lane >> 5;
     const int KT = a.K / (St::KK * NS * KSPL);   /* pipeline steps of this half (host: divisible) */
     const int kofs = khalf * KT;                 /* this half's first step */
@@ -171,13 +176,13 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
 
     /* per-lane global sources of this wave's DMA slots for K-tile 0 of tile (m0, n0);
      * K-tile kt adds kt * its step */
-    const uint16_t *xsrc[FM];
+    const uint16_t *xsrc[St::AD];
     const uint8_t *wsrc[NWQ];
     const float *ssrc = nullptr;
     auto sources = [&](int m0, int n0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < FM; i++) {
-            const int p = 256 * i + 64 * wave + lane, r = p >> 3, cp = p & 7;
+        for (int i = 0; i < St::AD; i++) {
+            const int p = 256 * NSP * i + 64 * wave + lane, r = p >> 3, cp = p & 7;
             const int c = cp ^ ((r >> 1) & 7);
             if constexpr (WT == ARIA_WI8)   /* int8 rows: K bytes, 16 k per chunk */
                 xsrc[i] = reinterpret_cast<const uint16_t *>((const int8_t *)a.x + (size_t)min(m0 + r, a.M - 1) * a.K + 16 * c);
@@ -211,14 +216,14 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
             const uint32_t st = sbase + B * SB + u * St::BYTES;
             if constexpr (WT == ARIA_WI8) {   /* 128 int8 k per K-tile: 128 bytes of every row */
 #pragma unroll
-                for (int i = 0; i < FM; i++)
-                    dma16(reinterpret_cast<const uint8_t *>(xsrc[i]) + k64 * 128, st + (256 * i + 64 * wave) * 16);
+                for (int i = 0; i < St::AD; i++)
+                    dma16(reinterpret_cast<const uint8_t *>(xsrc[i]) + k64 * 128, st + (256 * NSP * i + 64 * wave) * 16);
 #pragma unroll
                 for (int i = 0; i < NWQ; i++) dma16(wsrc[i] + k64 * 128, st + St::A + rbase * 128 + 1024 * i);
                 continue;
             }
 #pragma unroll
-            for (int i = 0; i < FM; i++) dma16(xsrc[i] + k64 * KB, st + (256 * i + 64 * wave) * 16);
+            for (int i = 0; i < St::AD; i++) dma16(xsrc[i] + k64 * KB, st + (256 * NSP * i + 64 * wave) * 16);
             if constexpr (WT == ARIA_WF16) {
 #pragma unroll
                 for (int i = 0; i < NWQ; i++) dma16(wsrc[i] + k64 * 128, st + St::A + rbase * 128 + 1024 * i);
@@ -433,42 +438,44 @@ __global__ __launch_bounds__(256 * KSPL, MINB) void k_qgemm_big(QArgs a, int NTN
 }
 
 /* NST = 0: three stages where they fit the LDS share of MINB workgroups, else two */
-template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int KSPL = 1, int NS = 1, int NST = 0>
+template <int WT, int FM, int FN, int MODE, bool GELU = false, int MINB = 1, int KSPL = 1, int NSP = 1, int NS = 1,
+          int NST = 0>
 static void launch_big_m(const QArgs &a, hipStream_t s) {
-    constexpr int BM = 32 * FM, BN = 128 * FN;
-    constexpr int NSTA = NST ? NST : (3 * KSPL * NS * Stage<WT, FM, FN>::BYTES <= 160 * 1024 / MINB ? 3 : 2);
+    constexpr int BM = 32 * FM, BN = 128 * FN * NSP;
+    constexpr int NSTA = NST ? NST : (3 * KSPL * NS * Stage<WT, FM, FN, NSP>::BYTES <= 160 * 1024 / MINB ? 3 : 2);
     const int MT = (a.M + BM - 1) / BM, NTN = (a.N + BN - 1) / BN, T = MT * NTN;
     const int grid = ((T + 7) / 8) * 8;
-    hipLaunchKernelGGL((k_qgemm_big<WT, FM, FN, MODE, GELU, MINB, NS, NSTA, KSPL>), dim3(grid), dim3(256 * KSPL), 0, s,
-                       a, NTN, T);
+    hipLaunchKernelGGL((k_qgemm_big<WT, FM, FN, MODE, GELU, MINB, NS, NSTA, KSPL, NSP>), dim3(grid),
+                       dim3(256 * KSPL * NSP), 0, s, a, NTN, T);
 }
 
 /* one kernel per fused epilogue mode (a run-time mode switch inside the store loop makes
  * every store wait for the loads of the modes that read); HEADS needs FN = 2 (a head's 64
  * columns in one wave) */
-template <int WT, int FM, int FN, int MINB, int KSPL = 1>
+template <int WT, int FM, int FN, int MINB, int KSPL = 1, int NSP = 1>
 static void launch_big(const QArgs &a, hipStream_t s) {
     switch (a.epi.mode) {
-        case ARIA_EPI_GATE_RES: launch_big_m<WT, FM, FN, ARIA_EPI_GATE_RES, false, MINB, KSPL>(a, s); break;
-        case ARIA_EPI_ADD: launch_big_m<WT, FM, FN, ARIA_EPI_ADD, false, MINB, KSPL>(a, s); break;
+        case ARIA_EPI_GATE_RES: launch_big_m<WT, FM, FN, ARIA_EPI_GATE_RES, false, MINB, KSPL, NSP>(a, s); break;
+        case ARIA_EPI_ADD: launch_big_m<WT, FM, FN, ARIA_EPI_ADD, false, MINB, KSPL, NSP>(a, s); break;
         case ARIA_EPI_ADD_DYT:
-            if constexpr (WT == ARIA_WF16) launch_big_m<WT, FM, FN, ARIA_EPI_ADD_DYT, false, MINB, KSPL>(a, s);
+            if constexpr (WT == ARIA_WF16) launch_big_m<WT, FM, FN, ARIA_EPI_ADD_DYT, false, MINB, KSPL, NSP>(a, s);
             break;
         case ARIA_EPI_HEADS:
-            if constexpr (FN >= 2) launch_big_m<WT, FM, FN, ARIA_EPI_HEADS, false, MINB, KSPL>(a, s);
+            if constexpr (FN >= 2) launch_big_m<WT, FM, FN, ARIA_EPI_HEADS, false, MINB, KSPL, NSP>(a, s);
             break;
-        case ARIA_EPI_GLU: launch_big_m<WT, FM, FN, ARIA_EPI_GLU, false, MINB, KSPL>(a, s); break;
+        case ARIA_EPI_GLU: launch_big_m<WT, FM, FN, ARIA_EPI_GLU, false, MINB, KSPL, NSP>(a, s); break;
         case ARIA_EPI_DYT_ROPE:
-            if constexpr (WT == ARIA_WF16) launch_big_m<WT, FM, FN, ARIA_EPI_DYT_ROPE, false, MINB, KSPL>(a, s);
+            if constexpr (WT == ARIA_WF16) launch_big_m<WT, FM, FN, ARIA_EPI_DYT_ROPE, false, MINB, KSPL, NSP>(a, s);
             break;
         default:
-            if (a.gelu) launch_big_m<WT, FM, FN, ARIA_EPI_STORE, true, MINB, KSPL>(a, s);
-            else launch_big_m<WT, FM, FN, ARIA_EPI_STORE, false, MINB, KSPL>(a, s);
+            if (a.gelu) launch_big_m<WT, FM, FN, ARIA_EPI_STORE, true, MINB, KSPL, NSP>(a, s);
+            else launch_big_m<WT, FM, FN, ARIA_EPI_STORE, false, MINB, KSPL, NSP>(a, s);
             break;
     }
 }
 
-/* the configurations compiled (FM, FN, workgroups per CU, K halves), index = the cfg argument;
+/* the configurations compiled (FM, FN, workgroups per CU, K halves, N halves), index = the cfg
+ * argument;
  * measured at M = 2592 (DiT shapes), fp16 activations:
  *   0: 96 x 128, two per CU: N <= 1024 with an odd number of K-tiles
  *   1: 128 x 128, two per CU: N = 3072 without HEADS
@@ -484,13 +491,19 @@ static void launch_big(const QArgs &a, hipStream_t s) {
  *      busy ones two waves per SIMD; ff_out Q4 42.8 -> 38.6 us, Q8 36.4 -> 33.3 us)
  *   6: 64 x 256 in 8-wave workgroups with the K range split the same way: HEADS with N <= 1024
  *      (ca_q, 164 tiles; 15.6 -> 15.2 us against configuration 2)
+ *   7: 192 x 256 in 8-wave workgroups, one per CU in three stages: each wave owns 32 weight
+ *      rows as in configuration 3, but the 8 waves share one activation tile, so a CU moves
+ *      24 KB of activations per K-tile instead of 48 and has the LDS for a third stage:
+ *      3072 < N <= 4096 (ff_in: 224 tiles; Q8 32.7 -> 30.5 us, Q4 34.9 -> 33.0 us at K = 1024,
+ *      -7 % at K = 2048, the same bits; at N = 8192 3-5 % slower than configuration 4)
  * Larger FM amortises each unpacked weight over more rows; 96 x 256, 64 x 128 and 192 x 256
  * (one per CU) measured slower at every DiT shape. */
-#define BIG_CFGS(X) X(0, 3, 1, 2, 1) X(1, 4, 1, 2, 1) X(2, 2, 2, 2, 1) X(3, 6, 1, 2, 1) X(4, 7, 1, 2, 1) X(5, 3, 1, 1, 2) \
-    X(6, 2, 2, 1, 2)
-static const int big_fm[] = {3, 4, 2, 6, 7, 3, 2};
-static const int big_fn[] = {1, 1, 2, 1, 1, 1, 2};
-static const int big_ks[] = {1, 1, 1, 1, 1, 2, 2};   /* 2: the K range split inside the workgroup */
+#define BIG_CFGS(X) X(0, 3, 1, 2, 1, 1) X(1, 4, 1, 2, 1, 1) X(2, 2, 2, 2, 1, 1) X(3, 6, 1, 2, 1, 1) X(4, 7, 1, 2, 1, 1) \
+    X(5, 3, 1, 1, 2, 1) X(6, 2, 2, 1, 2, 1) X(7, 6, 1, 1, 1, 2)
+static const int big_fm[] = {3, 4, 2, 6, 7, 3, 2, 6};
+static const int big_fn[] = {1, 1, 2, 1, 1, 1, 2, 1};
+static const int big_ks[] = {1, 1, 1, 1, 1, 2, 2, 1};    /* 2: the K range split inside the workgroup */
+static const int big_nsp[] = {1, 1, 1, 1, 1, 1, 1, 2};   /* 2: 8 waves, 256 FN weight rows */
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
 
@@ -535,17 +548,17 @@ static hipError_t qgemm_big_f16_launch(const QArgs &a, int cfg, hipStream_t s) {
     return hipGetLastError();
 }
 int qgemm_big_bm(int cfg) { return 32 * big_fm[cfg]; }
-int qgemm_big_bn(int cfg) { return 128 * big_fn[cfg]; }
+int qgemm_big_bn(int cfg) { return 128 * big_fn[cfg] * big_nsp[cfg]; }
 
 hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
     if (wt == ARIA_WF16 && a.K % KB == 0 && (!a.gelu || a.epi.mode == ARIA_EPI_STORE)) return qgemm_big_f16_launch(a, cfg, s);
     if (a.K % KB || cfg < 0 || cfg >= qgemm_big_ncfg() || (a.gelu && a.epi.mode != ARIA_EPI_STORE) ||
         (a.epi.mode == ARIA_EPI_HEADS && big_fn[cfg] < 2) || (a.K / KB) % big_ks[cfg])
         return hipErrorInvalidValue;
-#define BIG_CASE(i, fm, fn, mb, ks)                                        \
-    case i:                                                              \
-        if (wt == ARIA_WQ8) launch_big<ARIA_WQ8, fm, fn, mb, ks>(a, s);  \
-        else launch_big<ARIA_WQ4, fm, fn, mb, ks>(a, s);                 \
+#define BIG_CASE(i, fm, fn, mb, ks, nsp)                                        \
+    case i:                                                                   \
+        if (wt == ARIA_WQ8) launch_big<ARIA_WQ8, fm, fn, mb, ks, nsp>(a, s);  \
+        else launch_big<ARIA_WQ4, fm, fn, mb, ks, nsp>(a, s);                 \
         break;
     if (wt != ARIA_WQ8 && wt != ARIA_WQ4) return hipErrorInvalidValue;
     /* the Q4 [min, step] pairs of a K-tile move 16 bytes at a time */
@@ -570,15 +583,18 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
  *   4: 96 x 128 in 8-wave workgroups (the K range split, two stages each): N <= 1024 with
  *      K >= 2048 (ff_out: 23.6 -> 21.7 us)
  *   5: 64 x 256 in 8-wave workgroups, the K range split: HEADS with N <= 1024 (ca_q) */
-#define BIG_I8_CFGS(X) X(0, 2, 1, 2, 1) X(1, 2, 2, 2, 1) X(2, 4, 1, 2, 1) X(3, 6, 1, 2, 1) X(4, 3, 1, 1, 2) X(5, 2, 2, 1, 2)
-int qgemm_big_i8_ncfg() { return 6; }
+/* int8 (W8A8): the same forms with 128-deep K-tiles; 6 is configuration 7's 192 x 256 (N = 4096:
+ * 22.2 -> 21.6 us, GELU 24.3 -> 23.6 us at K = 1024, the same bits; no faster at N = 8192) */
+#define BIG_I8_CFGS(X) X(0, 2, 1, 2, 1, 1) X(1, 2, 2, 2, 1, 1) X(2, 4, 1, 2, 1, 1) X(3, 6, 1, 2, 1, 1) X(4, 3, 1, 1, 2, 1) \
+    X(5, 2, 2, 1, 2, 1) X(6, 6, 1, 1, 1, 2)
+int qgemm_big_i8_ncfg() { return 7; }
 
 hipError_t qgemm_big_i8_launch(const QArgs &a, int cfg, hipStream_t s) {
     if (a.K % 128 || (a.gelu && a.epi.mode != ARIA_EPI_STORE)) return hipErrorInvalidValue;
-#define BIG_I8_CASE(i, fm, fn, mb, ks)                                                       \
+#define BIG_I8_CASE(i, fm, fn, mb, ks, nsp)                                                  \
     case i:                                                                                \
         if ((a.epi.mode == ARIA_EPI_HEADS && fn < 2) || (a.K / 128) % ks) return hipErrorInvalidValue; \
-        launch_big<ARIA_WI8, fm, fn, mb, ks>(a, s);                                        \
+        launch_big<ARIA_WI8, fm, fn, mb, ks, nsp>(a, s);                                   \
         break;
     switch (cfg) {
         BIG_I8_CFGS(BIG_I8_CASE)

@@ -4,7 +4,7 @@ int8 MFMA GEMM) through the C ABI.
 Gate: bit-identical to the oracle's or_linear_q8a8 / or_quant_act_q8, which tests/test_oracle.py
 pins bit for bit to the compiled reference aria_linear_q8a8 (src/aria_quant.c:253-345) on the
 reference's own W8A8 shapes (tests/test_quant.c:146). Shapes cover every tile configuration
-(N <= 1024, <= 3072 and wider), ragged M / N edges, the SIMT form (K % 64 != 0, K % 4 != 0),
+(N <= 1024, <= 3072, <= 4096 and wider), ragged M / N edges, the SIMT form (K % 64 != 0, K % 4 != 0),
 zero rows (amax == 0) and the full config-3 sizes (checked on a subset of rows: the
 quantisation is per row).
 """
@@ -30,7 +30,7 @@ def ops(hip):
 
 SHAPES = [(1, 32, 1), (3, 64, 2), (4, 96, 3), (5, 100, 4), (7, 1030, 7), (9, 1024, 13), (12, 256, 6),
           (1, 64, 4), (33, 128, 260), (64, 64, 256), (130, 1024, 1000), (200, 1024, 3072), (64, 4096, 1024),
-          (97, 512, 512), (197, 256, 4100)]
+          (97, 512, 512), (197, 256, 4100), (197, 256, 3500)]
 
 
 @pytest.mark.parametrize("MKN", SHAPES)
