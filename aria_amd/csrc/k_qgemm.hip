@@ -411,8 +411,8 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
     if constexpr (WT != ARIA_WF16) {
         /* the LDS-DMA kernel (k_qgemm_big.hip): explicit tiles 13.. (configuration tiles - 13),
          * or picked for the shapes where it measured fastest: N <= 1024 without HEADS (96 x 128
-         * tiles, two workgroups per CU), HEADS with N <= 3072 (64 x 256, two per CU: the qkv and
-         * ca_q projections), other N <= 3072 without HEADS (128 x 128, two per CU), N = 4096
+         * tiles, two workgroups per CU), HEADS with N <= 3072 (the qkv projection: 64 x 512 in
+         * 8-wave workgroups, one per CU), other N <= 3072 without HEADS (128 x 128, two per CU), N = 4096
          * (192 x 256 in 8-wave workgroups, one per CU) and wider (224 x 128); N <= 1024 with an
          * even number of K-tiles in 96 x 128
          * tiles of 8 waves, the two halves of K on their own pipelines (216 tiles at M = 2592
@@ -424,7 +424,7 @@ static hipError_t launch_q(const QArgs &a, int tiles, hipStream_t s) {
         if (tiles == 0 && a.K % 64 == 0 && (WT != ARIA_WQ4 || ((uintptr_t)a.scale & 15u) == 0) &&
             (!a.gelu || a.epi.mode == ARIA_EPI_STORE)) {
             const bool heads = a.epi.mode == ARIA_EPI_HEADS;
-            const int cfg = heads ? (a.N <= 1024 && (a.K / 64) % 2 == 0 ? 6 : a.N <= 3072 ? 2 : -1)
+            const int cfg = heads ? (a.N <= 1024 && (a.K / 64) % 2 == 0 ? 6 : a.N <= 3072 ? 8 : -1)
                           : a.N <= 1024 ? ((a.K / 64) % 2 == 0 ? 5 : 0) : a.N <= 3072 ? 1 : a.N <= 4096 ? 7 : 4;
             if (cfg >= 0) return qgemm_big_launch(a, WT, cfg, s);
         }

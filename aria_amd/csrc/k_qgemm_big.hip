@@ -496,14 +496,17 @@ static void launch_big(const QArgs &a, hipStream_t s) {
  *      24 KB of activations per K-tile instead of 48 and has the LDS for a third stage:
  *      3072 < N <= 4096 (ff_in: 224 tiles; Q8 32.7 -> 30.5 us, Q4 34.9 -> 33.0 us at K = 1024,
  *      -7 % at K = 2048, the same bits; at N = 8192 3-5 % slower than configuration 4)
+ *   8: 64 x 512 in 8-wave workgroups, one per CU in three stages, each wave a head's 64 columns
+ *      (configuration 2's waves, sharing one activation tile): HEADS with 1024 < N <= 3072
+ *      (qkv: 246 tiles; 29.8 -> 28.8 us in the block, the same bits)
  * Larger FM amortises each unpacked weight over more rows; 96 x 256, 64 x 128 and 192 x 256
  * (one per CU) measured slower at every DiT shape. */
 #define BIG_CFGS(X) X(0, 3, 1, 2, 1, 1) X(1, 4, 1, 2, 1, 1) X(2, 2, 2, 2, 1, 1) X(3, 6, 1, 2, 1, 1) X(4, 7, 1, 2, 1, 1) \
-    X(5, 3, 1, 1, 2, 1) X(6, 2, 2, 1, 2, 1) X(7, 6, 1, 1, 1, 2)
-static const int big_fm[] = {3, 4, 2, 6, 7, 3, 2, 6};
-static const int big_fn[] = {1, 1, 2, 1, 1, 1, 2, 1};
-static const int big_ks[] = {1, 1, 1, 1, 1, 2, 2, 1};    /* 2: the K range split inside the workgroup */
-static const int big_nsp[] = {1, 1, 1, 1, 1, 1, 1, 2};   /* 2: 8 waves, 256 FN weight rows */
+    X(5, 3, 1, 1, 2, 1) X(6, 2, 2, 1, 2, 1) X(7, 6, 1, 1, 1, 2) X(8, 2, 2, 1, 1, 2)
+static const int big_fm[] = {3, 4, 2, 6, 7, 3, 2, 6, 2};
+static const int big_fn[] = {1, 1, 2, 1, 1, 1, 2, 1, 2};
+static const int big_ks[] = {1, 1, 1, 1, 1, 2, 2, 1, 1};    /* 2: the K range split inside the workgroup */
+static const int big_nsp[] = {1, 1, 1, 1, 1, 1, 1, 2, 2};   /* 2: 8 waves, 256 FN weight rows */
 
 int qgemm_big_ncfg() { return (int)(sizeof big_fm / sizeof big_fm[0]); }
 
@@ -584,7 +587,9 @@ hipError_t qgemm_big_launch(const QArgs &a, int wt, int cfg, hipStream_t s) {
  *      K >= 2048 (ff_out: 23.6 -> 21.7 us)
  *   5: 64 x 256 in 8-wave workgroups, the K range split: HEADS with N <= 1024 (ca_q) */
 /* int8 (W8A8): the same forms with 128-deep K-tiles; 6 is configuration 7's 192 x 256 (N = 4096:
- * 22.2 -> 21.6 us, GELU 24.3 -> 23.6 us at K = 1024, the same bits; no faster at N = 8192) */
+ * 22.2 -> 21.6 us, GELU 24.3 -> 23.6 us at K = 1024, the same bits; no faster at N = 8192).
+ * The int8 form of configuration 8 (64 x 512 HEADS, two stages of 72 KB) made the W8A8 qkv
+ * 21.1 -> 21.6 us: not compiled. */
 #define BIG_I8_CFGS(X) X(0, 2, 1, 2, 1, 1) X(1, 2, 2, 2, 1, 1) X(2, 4, 1, 2, 1, 1) X(3, 6, 1, 2, 1, 1) X(4, 3, 1, 1, 2, 1) \
     X(5, 2, 2, 1, 2, 1) X(6, 6, 1, 1, 1, 2)
 int qgemm_big_i8_ncfg() { return 7; }

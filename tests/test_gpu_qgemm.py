@@ -136,14 +136,14 @@ def test_qgemm_every_tile_shape(hip, port, tiles, wtype):
         assert relerr_max(dy.to_host(), want) <= GATE, (tiles, wtype, xf16)
 
 
-@pytest.mark.parametrize("wtype,tiles", [(w, t) for w in (0, 1) for t in range(13, 21)] +
+@pytest.mark.parametrize("wtype,tiles", [(w, t) for w in (0, 1) for t in range(13, 22)] +
                          [(2, t) for t in range(13, 18)])
 def test_qgemm_lds_dma_tiles(hip, port, tiles, wtype):
-    """The LDS-DMA kernel's tile configurations (tiles 13.. = configuration tiles - 13; eight
-    for Q8/Q4, two with the K range split inside the workgroup and the last with 8 waves over
-    256 weight rows, and five for fp16 weights, some in two pipeline stages) with ragged M and
-    N edges, fp16 activations; fp16 weights against the float64 product of the same fp16
-    values."""
+    """The LDS-DMA kernel's tile configurations (tiles 13.. = configuration tiles - 13; nine
+    for Q8/Q4, two with the K range split inside the workgroup and the last two with 8 waves
+    over 256 or 512 weight rows, and five for fp16 weights, some in two pipeline stages) with
+    ragged M and N edges, fp16 activations; fp16 weights against the float64 product of the
+    same fp16 values."""
     from aria_amd.device import DeviceArray, sync
     r = rng(140 + tiles * 3 + wtype)
     M, K, N = 197, 384, 136
@@ -168,7 +168,7 @@ def test_qgemm_lds_dma_tiles(hip, port, tiles, wtype):
 @pytest.mark.parametrize("wtype,tiles,MKN", [(2, 13, (5000, 768, 4608)), (0, 13, (2592, 1024, 1024)),
                                              (1, 14, (2592, 1024, 3072)), (1, 16, (2592, 1024, 4096)),
                                              (0, 17, (2592, 1024, 8192)), (1, 18, (2592, 4096, 1024)),
-                                             (1, 20, (2592, 1024, 4096))])
+                                             (1, 20, (2592, 1024, 4096)), (0, 21, (2592, 1024, 3072))])
 def test_qgemm_lds_dma_repeatable(hip, port, wtype, tiles, MKN):
     """Repeated launches of the LDS-DMA kernel on the same inputs give the same bits. Its
     pipeline overwrites a stage by DMA one step after the stage was read, so an LDS read still
