@@ -337,11 +337,22 @@ extern "C" hipError_t aria_k_mod_chunks(float *mod, const float *tssg, const flo
 }
 
 /* fp32 -> fp16 RTNE (the reference's k_f32_to_f16 / aria_f32_to_f16_n) */
+/* fp32 -> fp16 staging of GEMM activations, streamed: wave g converts float4 [256 g, 256 g + 256),
+ * lane l the four at 256 g + l + 64 j, all four loads issued before any store (the index is
+ * clamped instead of guarded: a guarded load compiles to a branch that waits for each load
+ * before the next). The fp32 source is read once (non-temporal loads); the fp16 copy is read
+ * next by the GEMM and stored normally, so it stays in the caches for it. */
 __global__ __launch_bounds__(256) void k_f2h4(uint2 *y, const float4 *x, size_t n4) {
-    GRID_STRIDE(i, n4) {
-        const float4 v = x[i];
-        y[i] = make_uint2((uint32_t)f2h_bits(v.x) | ((uint32_t)f2h_bits(v.y) << 16),
-                          (uint32_t)f2h_bits(v.z) | ((uint32_t)f2h_bits(v.w) << 16));
+    const size_t base = ((size_t)blockIdx.x * 256 + (threadIdx.x & ~63u)) * 4 + (threadIdx.x & 63);
+    float4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = ld_nt(x + min(base + 64 * j, n4 - 1));
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const size_t i = base + 64 * j;
+        if (i < n4)
+            y[i] = make_uint2((uint32_t)f2h_bits(v[j].x) | ((uint32_t)f2h_bits(v[j].y) << 16),
+                              (uint32_t)f2h_bits(v[j].z) | ((uint32_t)f2h_bits(v[j].w) << 16));
     }
 }
 __global__ __launch_bounds__(256) void k_f2h(uint16_t *y, const float *x, size_t n) {
@@ -350,7 +361,8 @@ __global__ __launch_bounds__(256) void k_f2h(uint16_t *y, const float *x, size_t
 extern "C" hipError_t aria_k_f32_to_f16(uint16_t *y, const float *x, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
     if (n % 4 == 0 && al16(x) && ((uintptr_t)y & 7u) == 0)
-        hipLaunchKernelGGL(k_f2h4, stream_grid(n / 4), dim3(256), 0, s, (uint2 *)y, (const float4 *)x, n / 4);
+        hipLaunchKernelGGL(k_f2h4, dim3((unsigned)((n / 4 + 1023) / 1024)), dim3(256), 0, s, (uint2 *)y,
+                           (const float4 *)x, n / 4);
     else
         hipLaunchKernelGGL(k_f2h, stream_grid((n + 3) / 4), dim3(256), 0, s, y, x, n);
     return hipGetLastError();
