@@ -336,12 +336,13 @@ extern "C" hipError_t aria_k_mod_chunks(float *mod, const float *tssg, const flo
     return hipGetLastError();
 }
 
-/* fp32 -> fp16 RTNE (the reference's k_f32_to_f16 / aria_f32_to_f16_n) */
-/* fp32 -> fp16 staging of GEMM activations, streamed: wave g converts float4 [256 g, 256 g + 256),
- * lane l the four at 256 g + l + 64 j, all four loads issued before any store (the index is
- * clamped instead of guarded: a guarded load compiles to a branch that waits for each load
- * before the next). The fp32 source is read once (non-temporal loads); the fp16 copy is read
- * next by the GEMM and stored normally, so it stays in the caches for it. */
+/* fp32 -> fp16 RTNE (the reference's k_f32_to_f16 / aria_f32_to_f16_n): the GEMMs' staging of
+ * fp32 activations, and weight and K/V conversions at set-up. Streamed: wave g converts float4
+ * [256 g, 256 g + 256), lane l the four at 256 g + l + 64 j, all four loads issued before any
+ * store (the index is clamped instead of guarded: a guarded load compiles to a branch that
+ * waits for each load before the next). The fp32 source is read once (non-temporal loads); the
+ * fp16 copy is stored normally, so it stays in the caches for the GEMM that reads it next
+ * (non-temporal stores made the K = 4096 staging + GEMM 3 us slower). */
 __global__ __launch_bounds__(256) void k_f2h4(uint2 *y, const float4 *x, size_t n4) {
     const size_t base = ((size_t)blockIdx.x * 256 + (threadIdx.x & ~63u)) * 4 + (threadIdx.x & 63);
     float4 v[4];
