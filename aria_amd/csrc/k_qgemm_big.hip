@@ -475,15 +475,16 @@ static void launch_big(const QArgs &a, hipStream_t s) {
 }
 
 /* the configurations compiled (FM, FN, workgroups per CU, K halves, N halves), index = the cfg
- * argument;
- * measured at M = 2592 (DiT shapes), fp16 activations:
+ * argument; measured at M = 2592 (DiT shapes), fp16 activations (the ones no longer picked stay
+ * reachable as explicit tiles):
  *   0: 96 x 128, two per CU: N <= 1024 with an odd number of K-tiles
  *   1: 128 x 128, two per CU: N = 3072 without HEADS
- *   2: 64 x 256, two per CU: the HEADS projections (qkv N = 3072, ca_q N = 1024): a head's 64
- *      columns in one wave, and the second workgroup per CU covers the other's HEADS epilogue
- *      (block 214 -> 204 us against 128 x 256 for qkv and the weights-in-registers ca_q)
- *   3: 192 x 128, two per CU in two stages: N = 4096 (ff_in; 448 tiles fill the 512 slots
- *      once; Q8 36.5 -> 33.3 us, Q4 38.2 -> 36.0 us against the weights-in-registers kernel)
+ *   2: 64 x 256, two per CU: a head's 64 columns in one wave, the second workgroup per CU
+ *      covering the other's HEADS epilogue (block 214 -> 204 us against 128 x 256 for qkv and the
+ *      weights-in-registers ca_q); the HEADS projections now take 6 (ca_q) and 8 (qkv)
+ *   3: 192 x 128, two per CU in two stages: N = 4096 before configuration 7 (448 tiles fill the
+ *      512 slots once; Q8 36.5 -> 33.3 us, Q4 38.2 -> 36.0 us against the weights-in-registers
+ *      kernel)
  *   4: 224 x 128, two per CU in two stages: N > 4096 (the GLU ff_in, N = 8192: Q8 74.4 ->
  *      58.3 us, Q4 73.4 -> 63.5 us)
  *   5: 96 x 128 in 8-wave workgroups, one per CU, waves 4-7 on the second half of the K range:
