@@ -45,6 +45,15 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
     return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
 
+/* the value of lane l ^ 32 (lane = this lane's index in the wave): gfx950's
+ * v_permlane32_swap exchanges the wave's two 32-lane halves in registers, without the LDS
+ * round trip of ds_bpermute */
+__device__ __forceinline__ float xor32_f32(float v, int lane) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, lane < 32 ? r[1] : r[0]);
+}
+
 struct OpSum {
     template <typename T> __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
 };

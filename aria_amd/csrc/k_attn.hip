@@ -298,7 +298,7 @@ __global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(4)
         t1[10] = fmaxf(sc[1][14], sc[1][15]);
         float mt = max3f(max3f(t1[0], t1[1], t1[2]), max3f(t1[3], t1[4], t1[5]), max3f(t1[6], t1[7], t1[8]));
         mt = max3f(mt, t1[9], t1[10]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32, ARIA_WAVE)) * a.scale_log2;
+        mt = fmaxf(mt, xor32_f32(mt, lane)) * a.scale_log2;
         /* lazy rescale: the reference max only moves when the tile max exceeds it by more
          * than RESCALE_SLACK (probabilities stay <= 2^8, exact in fp16's range); the final
          * O / l is unchanged by the choice of reference */
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(4)
         }
     }
 
-    float lrow = lsum + __shfl_xor(lsum, 32, ARIA_WAVE);   /* the query's full row sum */
+    float lrow = lsum + xor32_f32(lsum, lane);   /* the query's full row sum */
 
     if constexpr (KS == 2) {
         /* merge: the second half hands (O, l, m) to the first through LDS (the tile buffers

@@ -186,12 +186,10 @@ __global__ __launch_bounds__(64 * DA_WAVES) void k_dec_attn_mfma(DecAttnArgs a, 
         float x0 = sc[0][v] * 0.125f, x1 = sc[1][v] * 0.125f;
         float x2 = lr < DEC_S - 32 ? sc[2][v] * 0.125f : -INFINITY;
         float mx = fmaxf(fmaxf(x0, x1), x2);
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        mx = grp_max<16>(mx);   /* DPP within the row of 16 lanes, no LDS round trip */
         x0 = exp_fast(x0 - mx); x1 = exp_fast(x1 - mx); x2 = exp_fast(x2 - mx);
         float sum = (x0 + x1) + x2;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o);
+        sum = grp_sum<16>(sum);
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
         const int row = 4 * lq + v;
         P[row * DA_PS + lr] = x0 * inv;
