@@ -309,3 +309,33 @@ def test_axpy_scale_addto(ops, port, ref, n):
         assert np.array_equal(ops.axpy(y, x, -3.25).view(np.uint32), ref.axpy(y, x, -3.25).view(np.uint32))
         assert np.array_equal(ops.scale(x, 0.7071).view(np.uint32), ref.scale(x, 0.7071).view(np.uint32))
         assert np.array_equal(ops.addto(y, x).view(np.uint32), ref.addto(y, x).view(np.uint32))
+
+
+# ------------------------------------------------------------------ fp32 -> fp16 staging
+
+@pytest.mark.parametrize("n", [4, 1020, 4096, 4100, 75648, 4097, 7])
+def test_f32_to_f16_bits(hip, n):
+    """aria_k_f32_to_f16 (the GEMMs' staging of fp32 activations, the weights' and K/V's
+    conversion at set-up) against numpy's round-to-nearest-even float16, bit for bit: the
+    streamed four-vectors-per-lane form (n % 4 == 0, ragged last wave at 4100 and 75648), the
+    scalar form (4097, 7), and values at every rounding case (ties, subnormals, overflow to
+    inf, signed zeros, inf, NaN)."""
+    import ctypes as C
+    from aria_amd.device import DeviceArray, sync
+    r = rng(900 + n)
+    x = (r.standard_normal(n) * np.exp2(r.integers(-26, 18, n))).astype(np.float32)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, 65520.0, 65519.996, 6.1e-5, 5.96e-8,
+                        2.98e-8, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, -(1.0 + 2.0 ** -11)], np.float32)
+    k = min(n, special.size)
+    x[:k] = special[:k]
+    f = hip.lib().aria_k_f32_to_f16
+    f.restype = C.c_int
+    f.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+    dx, dy = DeviceArray.from_host(x), DeviceArray(n, np.float16)
+    hip.check(f(dy.p, dx.p, n, None))
+    sync()
+    got, want = dy.to_host().view(np.uint16), x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(np.isnan(dy.to_host()), nan)
+    bad = np.flatnonzero((got != want) & ~nan)
+    assert bad.size == 0, (bad[:4], x[bad[:4]], got[bad[:4]], want[bad[:4]])
