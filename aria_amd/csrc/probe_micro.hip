@@ -15,6 +15,8 @@
  *   MICRO_LDS   8 ds_read_b128 per lane and iteration from a 16 KB LDS table -> bytes / s
  *   MICRO_L1    8 global_load_dwordx4 per lane and iteration from a 16 KB table per workgroup
  *               (resident in the CU's L1 after the first pass)                -> bytes / s
+ *   MICRO_MIX_FMA  4 MFMA chains + 32 v_fma_f32 per trip (128 + 128 SIMD cycles if issued alone)
+ *   MICRO_MIX_EXP  4 MFMA chains + 16 v_exp_f32 per trip (128 + 128)            -> trips / s
  */
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -65,6 +67,47 @@ __global__ __launch_bounds__(256) void k_micro_valu(float *out, int iters, float
     out[(size_t)blockIdx.x * 256 + t] = s;
 }
 
+/* MFMA chains and VALU chains in one wave: per trip 4 MFMAs (4 x 32 cycles of the matrix pipe)
+ * and 8 NV independent v_fma_f32 (OP 0) or v_exp_f32 (OP 1); whether the SIMD overlaps the two
+ * shows as a trip time near the larger of the two instead of their sum */
+template <int OP, int NV>
+__global__ __launch_bounds__(256) void k_micro_mix(float *out, int iters, float m, float k) {
+    const int t = threadIdx.x;
+    half8_m a, b;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        a[j] = (_Float16)(0.125f * (float)((t + j) & 7));
+        b[j] = (_Float16)(0.0625f * (float)((t * 3 + j) & 7));
+    }
+    f32x16_m c0, c1, c2, c3;
+#pragma unroll
+    for (int r = 0; r < 16; r++) { c0[r] = 0.0f; c1[r] = 0.0f; c2[r] = 0.0f; c3[r] = 0.0f; }
+    float x[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) x[c] = 0.5f + 0.001f * (float)(t + c);
+    for (int i = 0; i < iters; i++) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < NV; v++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                if (v == NV / 2 && c == 0) {
+                    c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
+                    c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c2, 0, 0, 0);
+                }
+                if constexpr (OP == 0) x[c] = __builtin_fmaf(x[c], m, k);
+                else x[c] = __builtin_amdgcn_exp2f(-x[c]);
+            }
+        c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c3, 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) s += (c0[r] + c1[r]) + (c2[r] + c3[r]);
+#pragma unroll
+    for (int c = 0; c < 8; c++) s += x[c];
+    out[(size_t)blockIdx.x * 256 + t] = s;
+}
+
 __global__ __launch_bounds__(256) void k_micro_lds(float *out, int iters) {
     __shared__ uint4 tab[1024];
     const int t = threadIdx.x;
@@ -109,7 +152,7 @@ __global__ __launch_bounds__(256) void k_micro_l1(float *out, const uint4 *tab, 
     out[(size_t)blockIdx.x * 256 + t] = (float)s;
 }
 
-/* One launch of probe `which` (MICRO_* above, 0..5) with `grid` workgroups of 256 lanes and
+/* One launch of probe `which` (MICRO_* above, 0..7) with `grid` workgroups of 256 lanes and
  * `iters` loop trips on `stream`; out: grid * 256 floats; tab (MICRO_L1 only): grid * 16 KB of
  * device memory. Returns the hipError_t code of the launch (0 on success). */
 extern "C" int aria_probe_micro(int which, int grid, int iters, float *out, const void *tab, void *stream) {
@@ -125,6 +168,8 @@ extern "C" int aria_probe_micro(int which, int grid, int iters, float *out, cons
             if (!tab) return hipErrorInvalidValue;
             hipLaunchKernelGGL(k_micro_l1, dim3(grid), dim3(256), 0, s, out, (const uint4 *)tab, iters);
             break;
+        case 6: hipLaunchKernelGGL((k_micro_mix<0, 4>), dim3(grid), dim3(256), 0, s, out, iters, 0.999f, 0.001f); break;
+        case 7: hipLaunchKernelGGL((k_micro_mix<1, 2>), dim3(grid), dim3(256), 0, s, out, iters, 0.999f, 0.001f); break;
         default: return hipErrorInvalidValue;
     }
     return (int)hipGetLastError();

@@ -625,6 +625,12 @@ def micro_leg(L, chk, DeviceArray, Timer, stream):
         t = run(which, g, it)
         byt = g * 4 * it * 8 * 64 * 16
         res[name] = {"bytes_per_clk_per_cu": round(byt / t / clk / cus, 1), "TB/s": round(byt / t / 1e12, 1)}
+    # 4 MFMAs (128 matrix-pipe cycles) and 128 cycles' worth of VALU per trip and wave: ~128
+    # cycles per trip if the SIMD overlaps the two, ~256 if it does not
+    for which, name in ((6, "mix_4mfma_32fma"), (7, "mix_4mfma_16exp")):
+        g, it = 1024, 4000
+        t = run(which, g, it)
+        res[name] = {"cycles_per_trip_per_wave_per_simd": round(clk * t / (g * 4 * it / simds), 1)}
     return res
 
 
