@@ -58,6 +58,8 @@ SIGNATURES = {
     "aria_hip_last_error": (C.c_char_p, []),
     "aria_hip_default_stream": (_P, []),
     "aria_hip_stream_sync": (_i, [_P]),
+    "aria_hip_stream_create": (_P, []),
+    "aria_hip_stream_destroy": (None, [_P]),
     "aria_hip_event_create": (_P, []),
     "aria_hip_event_destroy": (None, [_P]),
     "aria_hip_event_record": (_i, [_P, _P]),

@@ -127,6 +127,16 @@ int aria_hip_stream_sync(void *stream) {
     return 0;
 }
 
+void *aria_hip_stream_create(void) {
+    if (ensure()) return NULL;
+    hipStream_t st = NULL;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return NULL;
+    return (void *)st;
+}
+void aria_hip_stream_destroy(void *stream) {
+    if (stream && stream != (void *)g_stream) hipStreamDestroy((hipStream_t)stream);
+}
+
 void *aria_hip_event_create(void) {
     if (ensure()) return NULL;
     hipEvent_t ev = NULL;

@@ -11,8 +11,12 @@
  * device; every kernel argument and copy uses that address.
  *
  * Every call on one GPU shares that GPU's array and the array keeps the last call's
- * contents: calls that overlap on one GPU (two streams, two threads) race on it. The
- * staging is fully written before the GEMM reads it, so nothing needs clearing.
+ * contents. The staging is fully written before the GEMM reads it, so nothing needs
+ * clearing. Calls from several streams are ordered on the device: each staging call records
+ * an event after its GEMM, and a call on another stream than the previous one first makes its
+ * stream wait for that event (one mutex covers the wait, the launches and the record, so two
+ * host threads cannot interleave them). A stream under capture records and waits for nothing
+ * (an event from outside a capture cannot join its graph): there the graph orders the calls.
  */
 #include <hip/hip_runtime.h>
 
@@ -33,9 +37,13 @@ static __device__ __align__(256) unsigned char scratch[ARIA_HIP_NOALLOC_SCRATCH]
 #define NOALLOC_MAX_DEV 64
 static std::mutex g_mu;
 static void *g_ptr[NOALLOC_MAX_DEV];   /* device address of `scratch`, per device */
+static hipEvent_t g_done[NOALLOC_MAX_DEV];   /* recorded after the last staging call's GEMM */
+static hipStream_t g_last[NOALLOC_MAX_DEV];  /* that call's stream */
+static bool g_used[NOALLOC_MAX_DEV];
 
-/* the current device's scratch address, resolved on the first call on that device */
-static int scratch_addr(void **out) {
+/* the current device's scratch address and ordering event, set up on the first call on that
+ * device; called with g_mu held */
+static int scratch_addr(void **out, int *devp) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return aria_hip_fail(e, "hipGetDevice");
@@ -44,15 +52,17 @@ static int scratch_addr(void **out) {
                            NOALLOC_MAX_DEV);
         return ARIA_HIP_EINVAL;
     }
-    std::lock_guard<std::mutex> lk(g_mu);
     if (!g_ptr[dev]) {
         void *p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p) return aria_hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
                                                         "hipGetSymbolAddress (scratch)");
+        if ((e = hipEventCreateWithFlags(&g_done[dev], hipEventDisableTiming)) != hipSuccess)
+            return aria_hip_fail(e, "hipEventCreateWithFlags (no-alloc ordering)");
         g_ptr[dev] = p;
     }
     *out = g_ptr[dev];
+    *devp = dev;
     return 0;
 }
 
@@ -80,12 +90,27 @@ extern "C" int aria_hip_qlinear_noalloc_dev(void *dy, int y_f16, const void *dx,
                                M, K, need, (size_t)ARIA_HIP_NOALLOC_SCRATCH);
             return ARIA_HIP_EINVAL;
         }
+        std::lock_guard<std::mutex> lk(g_mu);
         void *p = nullptr;
-        if ((rc = scratch_addr(&p))) return rc;
-        hipError_t e = aria_k_f32_to_f16((uint16_t *)p, (const float *)dx, (size_t)M * K, s);
-        if (e != hipSuccess) return aria_hip_fail(e, "k_f32_to_f16 (scratch staging)");
-        xa = p;
-        xh = 1;
+        int dev = 0;
+        if ((rc = scratch_addr(&p, &dev))) return rc;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        hipError_t e = hipStreamIsCapturing(s, &cs);
+        if (e != hipSuccess) return aria_hip_fail(e, "hipStreamIsCapturing");
+        const bool order = cs == hipStreamCaptureStatusNone;
+        if (order && g_used[dev] && g_last[dev] != s && (e = hipStreamWaitEvent(s, g_done[dev], 0)) != hipSuccess)
+            return aria_hip_fail(e, "hipStreamWaitEvent (no-alloc ordering)");
+        if ((e = aria_k_f32_to_f16((uint16_t *)p, (const float *)dx, (size_t)M * K, s)) != hipSuccess)
+            return aria_hip_fail(e, "k_f32_to_f16 (scratch staging)");
+        if ((e = aria_k_qgemm_t(dy, y_f16, p, 1, wtype, dq, dscale, db, M, K, N, 0, 0, s)) != hipSuccess)
+            return aria_hip_fail(e, "k_qgemm (no-alloc)");
+        if (order) {
+            if ((e = hipEventRecord(g_done[dev], s)) != hipSuccess)
+                return aria_hip_fail(e, "hipEventRecord (no-alloc ordering)");
+            g_last[dev] = s;
+            g_used[dev] = true;
+        }
+        return 0;
     }
     hipError_t e = aria_k_qgemm_t(dy, y_f16, xa, xh, wtype, dq, dscale, db, M, K, N, 0, 0, s);
     if (e != hipSuccess) return aria_hip_fail(e, "k_qgemm (no-alloc)");

@@ -42,6 +42,10 @@ int aria_hip_init(void);
 const char *aria_hip_last_error(void);
 void *aria_hip_default_stream(void);
 int aria_hip_stream_sync(void *stream);
+/* A further stream (non-blocking, default priority) for callers that run work side by side, or
+ * NULL; aria_hip_stream_destroy ignores NULL and the library's own stream. */
+void *aria_hip_stream_create(void);
+void aria_hip_stream_destroy(void *stream);
 /* HIP events for stream-ordered timing (bench harness). */
 void *aria_hip_event_create(void);
 void aria_hip_event_destroy(void *ev);
@@ -152,8 +156,10 @@ int aria_hip_linear_q8_dev(float *dy, const float *dx, const int8_t *dq, const f
  * fp16 staging of fp32 activations goes to a static device array of
  * ARIA_HIP_NOALLOC_SCRATCH bytes per GPU instead of per-call pool memory, so M * K * 2 must
  * not exceed it (ARIA_HIP_EINVAL otherwise; fp16 activations need no staging). Every call
- * on one GPU shares that array: calls that overlap on one GPU (other streams or threads)
- * race and must be serialised by the caller. */
+ * on one GPU shares that array. A staging call on another stream than the GPU's previous one
+ * first waits (hipStreamWaitEvent) for that call's GEMM, so calls from several streams or
+ * threads run one after another on the device. Under stream capture the call records no
+ * event and waits for none: inside a graph the caller orders the calls. */
 #define ARIA_HIP_NOALLOC_SCRATCH ((size_t)32 << 20)
 int aria_hip_qlinear_noalloc_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype, const void *dq,
                                  const float *dscale, const float *db, int M, int K, int N, void *stream);
