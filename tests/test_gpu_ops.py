@@ -168,9 +168,10 @@ def test_rope_golden(ops, golden):
 
 def test_rope_shapes(ops, port):
     r = rng(15)
-    # the vector kernel rotates 4, 2 or 1 head rows per thread as H allows (4 | H, 2 | H, odd H)
+    # the vector kernel rotates 4, 2 or 1 head rows per thread as H allows (4 | H, 2 | H, odd H);
+    # rot 24 leaves lanes of each workgroup idle (3 lanes per position), rot 128 takes 16
     for (H, N, D, rot) in [(4, 60, 64, 32), (32, 1296, 64, 32), (32, 1296, 64, 64), (3, 17, 20, 6),
-                           (2, 33, 64, 32), (5, 41, 64, 64), (6, 20, 72, 16)]:
+                           (2, 33, 64, 32), (5, 41, 64, 64), (6, 20, 72, 16), (8, 70, 64, 24), (4, 50, 128, 128)]:
         c, s = port.rope_freqs(N, rot, 10000.0)
         x = randn(r, (H, N, D))
         got = ops.rope_apply(x, c, s, rot)
