@@ -631,6 +631,12 @@ def micro_leg(L, chk, DeviceArray, Timer, stream):
         g, it = 1024, 4000
         t = run(which, g, it)
         res[name] = {"cycles_per_trip_per_wave_per_simd": round(clk * t / (g * 4 * it / simds), 1)}
+    # the same with one wave per SIMD (256 workgroups of 4 waves): whether one wave's VALU runs
+    # under its own MFMAs (the MFMA-only probe gives the matrix pipe's 128 cycles per trip)
+    for which, name in ((0, "mfma_only_1wave"), (6, "mix_4mfma_32fma_1wave"), (7, "mix_4mfma_16exp_1wave")):
+        g, it = 256, 4000
+        t = run(which, g, it)
+        res[name] = {"cycles_per_trip": round(clk * t / it, 1)}
     return res
 
 
