@@ -134,6 +134,9 @@ def parse():
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="only the K-sweep of the config-3 dequant GEMMs (M = 2592, N 4096 / 1024, K 512-4096, "
                          "Q8 / Q4, fp16 activations) with the fit t = t0 + c * K / 64 per (weights, N)")
+    ap.add_argument("--dit-only", default="",
+                    help="only the 24-block DiT stack leg, in the given modes (comma list of graph, inline, "
+                         "graph_w8a8; inline alone for a kernel trace of the step)")
     ap.add_argument("--vendor", action="store_true",
                     help="only the vendor-library reference points: PyTorch's fp16 GEMM (hipBLASLt) and "
                          "scaled_dot_product_attention at this build's GEMM and attention shapes")
@@ -337,6 +340,10 @@ def main():
     rng = np.random.default_rng(SEED)
     if args.gemm_sweep:
         print(json.dumps({"gemm_sweep": gemm_sweep_leg(L, chk, DeviceArray, Timer, stream, rng)}), flush=True)
+        return
+    if args.dit_only:
+        modes = tuple(m for m in args.dit_only.split(",") if m)
+        print(json.dumps({"dit": dit_leg(DeviceArray, Timer, L, chk, stream, rng, modes=modes)}), flush=True)
         return
     if args.micro:
         print(json.dumps({"micro": micro_leg(L, chk, DeviceArray, Timer, stream)}), flush=True)
@@ -918,7 +925,7 @@ def dec_leg(DeviceArray, Timer, rng, reps=10):
     return out
 
 
-def dit_leg(DeviceArray, Timer, L, chk, stream, rng, steps=8, depth=24):
+def dit_leg(DeviceArray, Timer, L, chk, stream, rng, steps=8, depth=24, modes=("graph", "inline", "graph_w8a8")):
     """Config 5: a 24-block random-init q4 DiT stack (config-4 block shape, tanh-GELU 4x FFN, one
     seed stream for all blocks) at T = 1296, batch 2 (the CFG pair as one batched request),
     latent [2, 64, 1296] ~N(0,1), project_in [1024,64], project_out [64,1024], pre/post 1x1
@@ -941,7 +948,9 @@ def dit_leg(DeviceArray, Timer, L, chk, stream, rng, steps=8, depth=24):
     gall = (0.1 * rng.standard_normal((steps, Bb, 6 * ed))).astype(np.float32)
     sched = np.linspace(1.0, 0.0, steps + 1).astype(np.float32)
     out = {"depth": depth, "T": T, "batch": Bb, "io_ch": C, "steps": steps, "ffn": "gelu4x", "precision": "q4"}
-    for mode in ("graph", "inline", "graph_w8a8"):
+    for mode in modes:
+        if mode not in ("graph", "inline", "graph_w8a8"):
+            raise SystemExit(f"unknown DiT mode {mode}")
         if mode == "inline":
             os.environ["ARIA_NO_GRAPH"] = "1"
         try:
@@ -989,7 +998,8 @@ def dit_leg(DeviceArray, Timer, L, chk, stream, rng, steps=8, depth=24):
         + 2 * 2.0 * Bb * H * T * T * 64 + 2 * 2.0 * Bb * H * T * Sc * 64
     flop = depth * blk + 2 * 2.0 * Bb * T * C * ed + 2 * 2.0 * Bb * T * C * C
     out["flop_per_step"] = flop
-    out["TFLOP/s_graph"] = round(flop / (out["graph_ms_per_step"] * 1e-3) / 1e12, 1)
+    for mode in modes:
+        out[f"TFLOP/s_{mode}"] = round(flop / (out[f"{mode}_ms_per_step"] * 1e-3) / 1e12, 1)
     return out
 
 
