@@ -302,14 +302,15 @@ int aria_hip_dit_block_cross_kv_dev(aria_hip_dit_block *b, const float *dctx, in
 
 static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const float *dgcond, const uint16_t *dk,
                          const uint16_t *dv, int Sc, const float *dcos, const float *dsin, int rot,
-                         const float *dlocal, void *dws, size_t ws_bytes, hipStream_t s);
+                         const float *dlocal, void *dws, size_t ws_bytes, const aria_hip_dit_block *next,
+                         hipStream_t s);
 
 int aria_hip_dit_block_forward_dev(aria_hip_dit_block *b, float *dx, int B, int S, const float *dgcond,
                                    const uint16_t *dk, const uint16_t *dv, int Sc, const float *dcos,
                                    const float *dsin, int rot, void *dws, size_t ws_bytes, void *stream) {
     int rc = aria_hip_ensure();
     if (rc) return rc;
-    return block_forward(b, dx, B, S, dgcond, dk, dv, Sc, dcos, dsin, rot, NULL, dws, ws_bytes,
+    return block_forward(b, dx, B, S, dgcond, dk, dv, Sc, dcos, dsin, rot, NULL, dws, ws_bytes, NULL,
                          aria_hip_stream(stream));
 }
 
@@ -326,12 +327,35 @@ static hipError_t gemm_i8(const dmat *m, float *y, const wsl *w, const float *bi
  * scales directly, and the attention outputs and the FFN product, whose rows span many
  * workgroups, are written fp32 and quantised by aria_k_quant_act_q8. The int8 GEMMs carry the
  * same fused epilogues (heads, gated residual, residual + local cond, GLU / GELU). */
+/* bytes of a packed matrix and of its scales */
+static size_t dm_qbytes(const dmat *m) {
+    return m->wtype == ARIA_WQ8 ? (size_t)m->N * m->K
+         : m->wtype == ARIA_WQ4 ? (size_t)m->N * ((m->K + 1) / 2) : (size_t)m->N * m->K * 2;
+}
+static size_t dm_sbytes(const dmat *m) {
+    return m->wtype == ARIA_WQ8 ? (size_t)m->N * 4 : m->wtype == ARIA_WQ4 ? (size_t)m->N * 2 * ((m->K + 31) / 32) * 4 : 0;
+}
+
+/* the next block's projection weights, read by the self-attention launch on the CUs it leaves
+ * idle: inside a DiT step the 24 blocks' weights do not stay in the 256 MB Infinity Cache, and
+ * each block's GEMMs would otherwise fetch theirs from HBM as they run */
+static void next_weights(const aria_hip_dit_block *nb, aria_prefetch_set *pf) {
+    pf->n = 0;
+    if (!nb) return;
+    const dmat *ms[] = {&nb->sa_qkv, &nb->sa_out, &nb->ca_q, &nb->ca_out, &nb->ff_in, &nb->ff_out};
+    for (size_t i = 0; i < sizeof ms / sizeof *ms && pf->n + 2 <= ARIA_PF_SPANS; i++) {
+        pf->p[pf->n] = ms[i]->q; pf->bytes[pf->n++] = dm_qbytes(ms[i]) & ~(size_t)15;
+        pf->p[pf->n] = ms[i]->scale; pf->bytes[pf->n++] = dm_sbytes(ms[i]) & ~(size_t)15;
+    }
+}
+
 /* the widths whose rows the norm kernel holds in registers (and can quantise there) */
 static int w8_fused_norm(int d) { return d == 256 || d == 512 || d == 768 || d == 1024 || d == 2048; }
 
 static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int B, int S, const float *const *tc,
                             const float *const *gc, int gbs, const uint16_t *dk, const uint16_t *dv, int Sc,
-                            const float *dcos, const float *dsin, int rot, const float *dlocal, hipStream_t s) {
+                            const float *dcos, const float *dsin, int rot, const float *dlocal,
+                            const aria_prefetch_set *pf, hipStream_t s) {
     const int d = b->dim, H = b->H, M = B * S;
     const float eps_norm = 1e-5f, eps_qk = 1e-6f;
 
@@ -353,7 +377,7 @@ static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int 
         const aria_qgemm_epi e = epi_heads(S, H, 3, kind, dst, nw, dcos, dsin, rot, eps_qk);
         STEP(gemm_i8(&b->sa_qkv, NULL, w, NULL, M, 0, &e, s), "k_gemm_i8 (sa_to_qkv + heads)");
     }
-    STEP(aria_k_flash_attn(w->q16, w->k16, w->v16, w->f32, 0, B * H, H, S, S, s), "k_flash_attn (self)");
+    STEP(aria_k_flash_attn_pf(w->q16, w->k16, w->v16, w->f32, 0, B * H, H, S, S, pf, s), "k_flash_attn (self)");
     STEP(aria_k_quant_act_q8(w->xq, w->sx, w->f32, 0, M, d, s), "k_quant_act_q8 (self merge)");
     {
         const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, tc[2], gc[2], gbs, NULL);
@@ -412,7 +436,8 @@ static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int 
  * (src/aria_sa3_dit.c:248-252), or NULL */
 static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const float *dgcond, const uint16_t *dk,
                          const uint16_t *dv, int Sc, const float *dcos, const float *dsin, int rot,
-                         const float *dlocal, void *dws, size_t ws_bytes, hipStream_t s) {
+                         const float *dlocal, void *dws, size_t ws_bytes, const aria_hip_dit_block *next,
+                         hipStream_t s) {
     if (!b || B <= 0 || S <= 0 || Sc <= 0 || !dx || !dk || !dv || !dws || (rot && (!dcos || !dsin)) ||
         (rot != 0 && rot != 32 && rot != 64)) {
         aria_hip_set_error("aria_hip_dit_block_forward_dev: invalid argument");
@@ -435,7 +460,9 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
         gc[c] = dgcond ? dgcond + (size_t)c * d : NULL;
     }
     const int gbs = 6 * d;
-    if (b->w8) return block_forward_w8(b, &w, dx, B, S, tc, gc, gbs, dk, dv, Sc, dcos, dsin, rot, dlocal, s);
+    aria_prefetch_set pf;
+    next_weights(next, &pf);
+    if (b->w8) return block_forward_w8(b, &w, dx, B, S, tc, gc, gbs, dk, dv, Sc, dcos, dsin, rot, dlocal, &pf, s);
 
     /* ---- self-attention ---- */
     STEP(aria_k_rownorm_ada(w.h16, 1, dx, b->pre_norm, tc[0], tc[1], gc[0], gc[1], gbs, S, M, d, eps_norm, s),
@@ -447,7 +474,7 @@ static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const f
         const aria_qgemm_epi e = epi_heads(S, H, 3, kind, dst, nw, dcos, dsin, rot, eps_qk);
         STEP(gemm_e(&b->sa_qkv, NULL, w.h16, NULL, M, &e, s), "k_qgemm (sa_to_qkv + heads)");
     }
-    STEP(aria_k_flash_attn(w.q16, w.k16, w.v16, w.att16, 1, B * H, H, S, S, s), "k_flash_attn (self)");
+    STEP(aria_k_flash_attn_pf(w.q16, w.k16, w.v16, w.att16, 1, B * H, H, S, S, &pf, s), "k_flash_attn (self)");
     {   /* x += (att . sa_to_out^T) * sigmoid(1 - gate_self) */
         const aria_qgemm_epi e = epi_resid(ARIA_EPI_GATE_RES, S, tc[2], gc[2], gbs, NULL);
         STEP(gemm_e(&b->sa_out, dx, w.att16, NULL, M, &e, s), "k_qgemm (sa_to_out + gated residual)");
@@ -846,7 +873,8 @@ static int step_compute(aria_cuda_dit *h, hipStream_t s) {
             return rc;
     for (int b = 0; b < h->depth; b++) {
         rc = block_forward(h->blk[b], h->dseq, B, S, h->dgcond, h->ck[b], h->cv[b], h->Sc, h->cos_t, h->sin_t,
-                           h->rot, h->local ? h->local[b] : NULL, h->ws, h->ws_bytes, s);
+                           h->rot, h->local ? h->local[b] : NULL, h->ws, h->ws_bytes,
+                           b + 1 < h->depth ? h->blk[b + 1] : NULL, s);
         if (rc) return rc;
     }
     for (int b = 0; b < nb; b++)

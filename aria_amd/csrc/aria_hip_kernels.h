@@ -178,6 +178,18 @@ hipError_t aria_k_qkv_prep(const float *src, int ld, int B, int S, int H, int ns
  * (merged heads, fp16 when o_f16 else fp32), scale 1/8 */
 hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, const uint16_t *v, void *o, int o_f16,
                              int BH, int H, int Nq, int Nk, hipStream_t s);
+/* memory read (and discarded) by workgroups added to an attention launch on the CUs its own
+ * workgroups leave idle, so that it passes through the memory-side cache before a later
+ * kernel reads it (up to ARIA_PF_SPANS spans; bytes a multiple of 16, 16-byte aligned) */
+#define ARIA_PF_SPANS 12
+typedef struct {
+    const void *p[ARIA_PF_SPANS];
+    size_t bytes[ARIA_PF_SPANS];
+    int n;
+} aria_prefetch_set;
+/* aria_k_flash_attn that also prefetches pf (NULL: none) on the CUs the split form leaves idle */
+hipError_t aria_k_flash_attn_pf(const uint16_t *q, const uint16_t *k, const uint16_t *v, void *o, int o_f16,
+                                int BH, int H, int Nq, int Nk, const aria_prefetch_set *pf, hipStream_t s);
 
 /* fp32 SIMT GEMM (k_sgemm.hip), batched with element strides sA/sB/sC:
  * C_b[M,N] = alpha * (A_b[M,K] op(B_b)) (+ bias[N]); op(B) = B^T for B_b [N,K]

@@ -139,7 +139,39 @@ struct AttnArgs {
     int nqb, T;                  /* query blocks (32 QW queries) per (batch, head); nqb * B*H */
     float scale_log2;            /* (1/sqrt(64)) * log2(e) */
     int o_f16;
+    /* prefetch workgroups: blocks Tpad .. gridDim.x - 1 read pf[0 .. npf) and exit */
+    int Tpad, npf;
+    const uint4 *pf[ARIA_PF_SPANS];
+    unsigned pf_n16[ARIA_PF_SPANS];
 };
+
+#ifndef ARIA_ATTN_PF_NT
+#define ARIA_ATTN_PF_NT 0
+#endif
+/* prefetch workgroup w of nw: its share of every span, 4 16-byte loads per lane in flight; the
+ * values only feed an empty asm statement, which keeps the loads */
+__device__ __forceinline__ void attn_prefetch(const AttnArgs &a, int w, int nw) {
+    for (int sp = 0; sp < a.npf; sp++) {
+        const unsigned n = a.pf_n16[sp], per = (n + nw - 1) / nw, lo = min(n, w * per), hi = min(n, lo + per);
+        const uint4 *p = a.pf[sp];
+        for (unsigned i = lo + threadIdx.x; i < hi; i += 4 * blockDim.x) {
+            uint4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const unsigned k = min(i + j * blockDim.x, hi - 1);
+                if constexpr (ARIA_ATTN_PF_NT) {
+                    typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+                    const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p + k));
+                    v[j] = make_uint4(t.x, t.y, t.z, t.w);
+                } else {
+                    v[j] = p[k];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) asm volatile("" ::"v"(v[j].x));
+        }
+    }
+}
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
@@ -202,6 +234,10 @@ __global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(4)
     uint16_t *const Kb0 = Kb0s + half * (KT * 64), *const Kb1 = Kb1s + half * (KT * 64);
     uint16_t *const Vb0 = Vb0s + half * (KT * 64), *const Vb1 = Vb1s + half * (KT * 64);
     const int lane = threadIdx.x & 63, wave = wid % QW, g = lane >> 5, l32 = lane & 31;
+    if ((int)blockIdx.x >= a.Tpad) {        /* a prefetch workgroup (uniform, before any barrier) */
+        attn_prefetch(a, (int)blockIdx.x - a.Tpad, (int)gridDim.x - a.Tpad);
+        return;
+    }
     /* the query blocks of one (batch, head) run on one XCD, so its K and V are fetched
      * into that XCD's L2 once rather than into every XCD's */
     const int tix = xcd_tile(blockIdx.x, a.T);
@@ -360,8 +396,8 @@ __global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(4)
     __syncthreads();
     /* two tiles per trip so each LDS buffer is a fixed address; buffer b^1 was last read
      * one tile earlier, before that tile's closing barrier. A wave whose 32 queries all lie
-     * past Nq (the tail of the last query block: 1296 = 10 x 128 + 16) only stages tiles and
-     * meets the barriers; its products would never be stored. */
+     * past Nq (in the last query block: 1296 = 6 x 192 + 144, so that block's sixth wave)
+     * only stages tiles and meets the barriers; its products would never be stored. */
     const bool live = q0 < a.Nq;
     for (int t = 0; t < niter; t += 2) {
         if (t + 1 < nt) dma(kbase + (t + 1) * KT, Kb1, Vb1);
@@ -433,10 +469,20 @@ __global__ __launch_bounds__(64 * QW * KS) __attribute__((amdgpu_waves_per_eu(4)
     }
 }
 
-extern "C" hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, const uint16_t *v, void *o, int o_f16,
-                                        int BH, int H, int Nq, int Nk, hipStream_t s) {
+extern "C" hipError_t aria_k_flash_attn_pf(const uint16_t *q, const uint16_t *k, const uint16_t *v, void *o,
+                                           int o_f16, int BH, int H, int Nq, int Nk, const aria_prefetch_set *pf,
+                                           hipStream_t s) {
     if (BH <= 0 || Nq <= 0) return hipSuccess;
     AttnArgs a;
+    a.npf = 0;
+    if (pf && (pf->n < 0 || pf->n > ARIA_PF_SPANS)) return hipErrorInvalidValue;
+    for (int i = 0; pf && i < pf->n; i++) {
+        if (!pf->p[i] || !pf->bytes[i]) continue;
+        if ((pf->bytes[i] & 15u) || ((uintptr_t)pf->p[i] & 15u) || pf->bytes[i] / 16 > 0xFFFFFFFFu)
+            return hipErrorInvalidValue;
+        a.pf[a.npf] = (const uint4 *)pf->p[i];
+        a.pf_n16[a.npf++] = (unsigned)(pf->bytes[i] / 16);
+    }
     a.q = q; a.k = k; a.v = v; a.o = o; a.H = H; a.Nq = Nq; a.Nk = Nk; a.o_f16 = o_f16;
     a.scale_log2 = 0.125f * ARIA_LOG2E;
     /* split the keys inside the workgroup when there are enough tiles for both halves
@@ -458,7 +504,17 @@ extern "C" hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, co
     }
     a.nqb = (Nq + 32 * qw - 1) / (32 * qw);
     a.T = a.nqb * BH;
-    const dim3 grid((a.T + 7) / 8 * 8);
+    a.Tpad = (a.T + 7) / 8 * 8;
+    /* prefetch workgroups on the CUs the split form's one-per-CU workgroups leave idle */
+    static int ncu = 0;
+    if (!ncu) {
+        int dev = 0, n = 0;
+        ncu = (hipGetDevice(&dev) == hipSuccess &&
+               hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? n : -1;
+    }
+    const int npw = (split && a.npf && ncu > a.Tpad) ? (ncu - a.Tpad) / 8 * 8 : 0;
+    if (!npw) a.npf = 0;
+    const dim3 grid(a.Tpad + npw);
     if (split) {
         if (qw == 6) hipLaunchKernelGGL((k_flash_attn<2, 6>), grid, dim3(768), 0, s, a);
         else if (qw == 5) hipLaunchKernelGGL((k_flash_attn<2, 5>), grid, dim3(640), 0, s, a);
@@ -469,4 +525,9 @@ extern "C" hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, co
         hipLaunchKernelGGL((k_flash_attn<1, 4>), grid, dim3(256), 0, s, a);
     }
     return hipGetLastError();
+}
+
+extern "C" hipError_t aria_k_flash_attn(const uint16_t *q, const uint16_t *k, const uint16_t *v, void *o, int o_f16,
+                                        int BH, int H, int Nq, int Nk, hipStream_t s) {
+    return aria_k_flash_attn_pf(q, k, v, o, o_f16, BH, H, Nq, Nk, nullptr, s);
 }
