@@ -78,6 +78,9 @@ static void init_once(void) {
         return;
     }
     g_ok = 1;
+    /* the allocation-free GEMM's scratch address and ordering event; a failure here is
+     * reported by that entry point, which retries the set-up on its first call */
+    if (aria_noalloc_setup()) hipGetLastError();
 }
 
 /* make the library device current on the calling thread; 0 or ENODEV */

@@ -17,5 +17,8 @@ ARIA_HIDDEN int aria_hip_fail(hipError_t e, const char *what);
 ARIA_HIDDEN void aria_hip_set_error(const char *fmt, ...);
 /* the stream to use for a caller's void* (NULL = library stream) */
 ARIA_HIDDEN hipStream_t aria_hip_stream(void *stream);
+/* the allocation-free GEMM's per-device set-up (k_noalloc.hip) for the current device, run at
+ * library init so that a first call under stream capture finds it done; 0 or an error code */
+ARIA_HIDDEN int aria_noalloc_setup(void);
 
 #endif /* ARIA_HIP_INTERNAL_H */

@@ -7,8 +7,9 @@
  * hipMalloc) call aria_hip_qlinear_noalloc_dev instead: the staging lives in `scratch`,
  * a file-scope device array of ARIA_HIP_NOALLOC_SCRATCH bytes that each GPU holds for the
  * life of the process. Its device address is resolved once per device with
- * hipGetSymbolAddress (host code sees only a stand-in for the array's name) and kept per
- * device; every kernel argument and copy uses that address.
+ * hipGetSymbolAddress (host code sees only a stand-in for the array's name), at library init
+ * for the library's device and on the first call on any other, and kept per device; every
+ * kernel argument and copy uses that address.
  *
  * Every call on one GPU shares that GPU's array and the array keeps the last call's
  * contents. The staging is fully written before the GEMM reads it, so nothing needs
@@ -41,8 +42,8 @@ static hipEvent_t g_done[NOALLOC_MAX_DEV];   /* recorded after the last staging 
 static hipStream_t g_last[NOALLOC_MAX_DEV];  /* that call's stream */
 static bool g_used[NOALLOC_MAX_DEV];
 
-/* the current device's scratch address and ordering event, set up on the first call on that
- * device; called with g_mu held */
+/* the current device's scratch address and ordering event, set up at library init (the
+ * library's device) or on the first call on another device; called with g_mu held */
 static int scratch_addr(void **out, int *devp) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -66,6 +67,13 @@ static int scratch_addr(void **out, int *devp) {
     *out = g_ptr[dev];
     *devp = dev;
     return 0;
+}
+
+extern "C" int aria_noalloc_setup(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    void *p = nullptr;
+    int dev = 0;
+    return scratch_addr(&p, &dev);
 }
 
 extern "C" int aria_hip_qlinear_noalloc_dev(void *dy, int y_f16, const void *dx, int x_f16, int wtype,
