@@ -320,13 +320,6 @@ static hipError_t gemm_i8(const dmat *m, float *y, const wsl *w, const float *bi
     return aria_k_gemm_i8(y, 0, w->xq, w->sx, (const int8_t *)m->q, m->scale, bias, M, m->K, m->N, gelu, e, s);
 }
 
-/* The W8A8 block (precision ARIA_Q8A8: the reference's h->w8a8 path, src/aria_cuda.cu:1055-1147,
- * with aria_linear_q8a8's numbers): the same steps as block_forward with every projection on
- * int8 activations. The reference keeps its producers in fp32 and quantises that output per
- * row (gemm_w8a8); here the norms quantise their fp32 rows in registers and write int8 + row
- * scales directly, and the attention outputs and the FFN product, whose rows span many
- * workgroups, are written fp32 and quantised by aria_k_quant_act_q8. The int8 GEMMs carry the
- * same fused epilogues (heads, gated residual, residual + local cond, GLU / GELU). */
 /* bytes of a packed matrix and of its scales */
 static size_t dm_qbytes(const dmat *m) {
     return m->wtype == ARIA_WQ8 ? (size_t)m->N * m->K
@@ -349,6 +342,13 @@ static void next_weights(const aria_hip_dit_block *nb, aria_prefetch_set *pf) {
     }
 }
 
+/* The W8A8 block (precision ARIA_Q8A8: the reference's h->w8a8 path, src/aria_cuda.cu:1055-1147,
+ * with aria_linear_q8a8's numbers): the same steps as block_forward with every projection on
+ * int8 activations. The reference keeps its producers in fp32 and quantises that output per
+ * row (gemm_w8a8); here the norms quantise their fp32 rows in registers and write int8 + row
+ * scales directly, and the attention outputs and the FFN product, whose rows span many
+ * workgroups, are written fp32 and quantised by aria_k_quant_act_q8. The int8 GEMMs carry the
+ * same fused epilogues (heads, gated residual, residual + local cond, GLU / GELU). */
 /* the widths whose rows the norm kernel holds in registers (and can quantise there) */
 static int w8_fused_norm(int d) { return d == 256 || d == 512 || d == 768 || d == 1024 || d == 2048; }
 
@@ -433,7 +433,8 @@ static int block_forward_w8(aria_hip_dit_block *b, const wsl *w, float *dx, int 
 }
 
 /* dlocal: the inpaint local-additive conditioning [B*S, dim] added after the cross-attention
- * (src/aria_sa3_dit.c:248-252), or NULL */
+ * (src/aria_sa3_dit.c:248-252), or NULL; next: the block that runs after this one in a DiT
+ * step (its weights are prefetched during this block's self-attention), or NULL */
 static int block_forward(aria_hip_dit_block *b, float *dx, int B, int S, const float *dgcond, const uint16_t *dk,
                          const uint16_t *dv, int Sc, const float *dcos, const float *dsin, int rot,
                          const float *dlocal, void *dws, size_t ws_bytes, const aria_hip_dit_block *next,
